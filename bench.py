@@ -1,0 +1,227 @@
+#!/usr/bin/env python3
+"""Decode throughput of the MI355X decoder token loop (BASELINE metric: decode tok/s, 1B bf16, b=1 and b=32,
+plus achieved HBM GB/s against the MI355X peak).
+
+Workload of `value` ("C2"): 1B-class GQA decoder (vocab 32000, d 2048, 16 layers, 32/8 heads,
+head dim 64, SwiGLU 5632, RoPE base 10000), bf16 weights with f32 accumulation, batch 1, seeded N(0, 0.02) weights
+synthesised in HBM, a 128-token prompt of uniform random ids, greedy decode.  A step is one full token step on
+the GPU: embedding gather -> 16 fused layers -> final norm + LM head -> sampling -> id fed back, replayed from a
+HIP graph; exactly --steps steps are timed with HIP events on the library's compute stream after --warmup
+untimed steps.
+
+Also reported: the b=32 decode over a 2048-token seeded K/V prefix (configs[2], "C3"), the per-kernel roofline of
+the dominant kernel (gate/up projection) from event pairs around each launch, a streaming-copy bandwidth
+reference, and the CPU oracle timed on this host (single thread) on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+C2 = dict(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parameter_slots(cfg):
+    """LM wrapper parameter order (registration order): tokens, decoder layers, final norm, output head."""
+    d, H, KV, F, V = cfg["dimensions"], cfg["heads"], cfg["kv_heads"], cfg["hidden"], cfg["vocab"]
+    hd = d // H
+    names = [("tokens.weight", (V, d))]
+    for i in range(cfg["layers"]):
+        p = f"decoder.layer{i}."
+        names += [(p + "attention.query.weight", (H * hd, d)), (p + "attention.key.weight", (KV * hd, d)),
+                  (p + "attention.value.weight", (KV * hd, d)), (p + "attention.output.weight", (d, H * hd)),
+                  (p + "feedforward.gate.weight", (F, d)), (p + "feedforward.up.weight", (F, d)),
+                  (p + "feedforward.down.weight", (d, F)), (p + "attention_norm.weight", (d,)),
+                  (p + "feedforward_norm.weight", (d,))]
+    names += [("decoder.normalization.weight", (d,)), ("output.weight", (V, d))]
+    return names
+
+
+def build_model(ct, cfg, context, root=(1234, 0)):
+    """Seeded weights drawn directly in HBM: slot s gets 0.02 * randn(fold_in(root, s)) rounded to bf16."""
+    gpu = ct.device("gpu")
+    decoder = ct.transformer_decoder(cfg["layers"], cfg["dimensions"], cfg["heads"], cfg["kv_heads"], cfg["hidden"],
+                                     context, ct.BF16, gpu)
+    state, embedding, head = {}, None, None
+    for slot, (name, shape) in enumerate(parameter_slots(cfg)):
+        if name.endswith("norm.weight") or name == "decoder.normalization.weight":
+            continue  # RMSNorm weights keep their module default (ones)
+        w = ct.normal(ct.fold_in(root, slot), shape, 0.02, ct.BF16, gpu)
+        if name == "tokens.weight":
+            embedding = w
+        elif name == "output.weight":
+            head = w
+        else:
+            state[name[len("decoder."):]] = w
+    current = decoder.state()
+    for name, tensor in current.items():
+        state.setdefault(name, tensor)
+    decoder.load_state(state)
+    del state, current
+    lm = ct.DecoderLM(ct.embedding_from(embedding), decoder, ct.linear_from(head))
+    return decoder, lm
+
+
+def weight_bytes(cfg):
+    d, H, KV, F, V = cfg["dimensions"], cfg["heads"], cfg["kv_heads"], cfg["hidden"], cfg["vocab"]
+    hd = d // H
+    per_layer = (H * hd + 2 * KV * hd) * d + d * H * hd + 3 * F * d
+    return 2 * (cfg["layers"] * per_layer + V * d)  # LM head once; one embedding row per sequence is negligible
+
+
+def kv_bytes(cfg, batch, length):
+    hd = cfg["dimensions"] // cfg["heads"]
+    return 2 * batch * cfg["layers"] * 2 * cfg["kv_heads"] * hd * length  # bf16 K and V read
+
+
+def decode_b1(ct, steps, warmup):
+    context = 128 + 3 + warmup + steps + 8
+    decoder, lm = build_model(ct, C2, max(384, context))
+    prompt = np.random.default_rng(7).integers(0, C2["vocab"], size=(1, 128), dtype=np.int64)
+    cache = ct.DecoderCache(decoder)
+    ms, tokens = lm.benchmark(prompt, cache, warmup, steps, 0.0, (0, 0), True)
+    # mean cache length over the timed steps: prompt + tokens before them, + the step's own key
+    first = 128 + 3 + warmup
+    mean_len = first + (steps - 1) / 2.0
+    step_bytes = weight_bytes(C2) + kv_bytes(C2, 1, mean_len)
+    # per-kernel device time of eager single-token steps (event pair around every launch)
+    pcache = ct.DecoderCache(decoder)
+    lm.logits(prompt, pcache)
+    timings = lm.profile(prompt[:, -1:], pcache, 8)
+    return dict(ms=ms, step_bytes=step_bytes, timings=timings, tokens=tokens, mean_len=mean_len), decoder, lm
+
+
+def decode_b32(ct, lm, decoder, steps, warmup, prefix=2048):
+    """C3: batch 32, each sequence holding `prefix` cached tokens of seeded random K/V."""
+    B = 32
+    cache = ct.DecoderCache(decoder)
+    hd = C2["dimensions"] // C2["heads"]
+    for layer in range(C2["layers"]):
+        k = ct.normal(ct.fold_in((4242, 0), 2 * layer), [B, C2["kv_heads"], prefix, hd], 1.0, ct.BF16)
+        v = ct.normal(ct.fold_in((4242, 0), 2 * layer + 1), [B, C2["kv_heads"], prefix, hd], 1.0, ct.BF16)
+        cache.append(layer, k, v)
+        del k, v
+    ids = np.random.default_rng(8).integers(0, C2["vocab"], size=(B, 1), dtype=np.int64)
+    ms, _ = lm.benchmark(ids, cache, warmup, steps, 0.0, (0, 0), True)
+    mean_len = prefix + 3 + warmup + (steps - 1) / 2.0
+    return dict(ms=ms, step_bytes=weight_bytes(C2) + kv_bytes(C2, B, mean_len), batch=B, mean_len=mean_len)
+
+
+def cpu_baseline(prompt_len=4, decode_steps=8):
+    """The CPU oracle (plain-C restatement of the reference CPU path) on this host, one thread, at the C2 shape:
+    a short prompt is fed, then `decode_steps` single-token greedy steps are timed."""
+    import oracle
+    oracle.lib()
+    cfg = oracle.ModelConfig(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632,
+                             context=prompt_len + decode_steps + 1, dtype="bf16")
+    oracle.set_threads(min(16, os.cpu_count() or 1))
+    weights = oracle.synthesize_weights(cfg, (1234, 0))
+    lm = oracle.OracleLM(cfg, weights)
+    oracle.set_threads(1)
+    cache = lm.make_cache(1)
+    ids = np.random.default_rng(7).integers(0, cfg.vocab, size=(1, prompt_len), dtype=np.int64)
+    logits = lm.logits(ids, cache)
+    token = logits[:, -1].argmax(-1).reshape(1, 1)
+    t0 = time.perf_counter()
+    for _ in range(decode_steps):
+        logits = lm.logits(token, cache)
+        token = logits[:, -1].argmax(-1).reshape(1, 1)
+    elapsed = time.perf_counter() - t0
+    return dict(value=decode_steps / elapsed, unit="tok/s", cores=1, kind="port",
+                sample=f"1B bf16 b=1 (C2 shape), {prompt_len}-token prompt then {decode_steps} greedy decode steps "
+                       f"timed ({elapsed:.1f} s), oracle/oracle.c -O3 -ffp-contract=off, 1 thread")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--b32-steps", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-b32", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import ctorch_amd as ct
+    ct.lib()
+    log("bench: copy bandwidth probe")
+    copy_gbps = ct.copy_bandwidth(1 << 30, 20)
+    log(f"bench: streaming copy {copy_gbps:.0f} GB/s; building 1B bf16 model in HBM")
+    b1, decoder, lm = decode_b1(ct, args.steps, args.warmup)
+    ms_per_step = b1["ms"] / args.steps
+    tok_s = args.steps / (b1["ms"] / 1e3)
+    achieved = b1["step_bytes"] / (ms_per_step / 1e3) / 1e9
+    log(f"bench: b=1 {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tok/s, {achieved:.0f} GB/s algorithmic")
+
+    gate = next(t for t in b1["timings"] if t["name"] == "gate_up_silu")
+    gate_avg_ms = gate["total_ms"] / gate["launches"]
+    gate_bytes = gate["bytes"] / gate["launches"]
+    gate_gbps = gate_bytes / (gate_avg_ms / 1e3) / 1e9
+    kernels = {t["name"]: {"launches": t["launches"], "avg_us": 1e3 * t["total_ms"] / t["launches"],
+                           "GB/s": (t["bytes"] / t["total_ms"] * 1e-6) if t["total_ms"] > 0 and t["bytes"] else None}
+               for t in b1["timings"]}
+
+    extra = {}
+    if not args.no_b32:
+        log("bench: b=32 over a 2048-token prefix")
+        b32 = decode_b32(ct, lm, decoder, args.b32_steps, 4)
+        ms32 = b32["ms"] / args.b32_steps
+        extra["b32"] = {"tok_s": 32 * args.b32_steps / (b32["ms"] / 1e3), "ms_per_step": ms32,
+                        "achieved_GBps": b32["step_bytes"] / (ms32 / 1e3) / 1e9,
+                        "frac_of_peak": b32["step_bytes"] / (ms32 / 1e3) / 1e9 / HBM_PEAK_GBPS,
+                        "steps": args.b32_steps, "prefix": 2048}
+        log(f"bench: b=32 {ms32:.3f} ms/step, {extra['b32']['tok_s']:.0f} tok/s")
+    del lm, decoder
+
+    baseline = None
+    if not args.no_cpu_baseline:
+        log("bench: CPU oracle baseline (single thread, bounded sample)")
+        baseline = cpu_baseline()
+        log(f"bench: CPU {baseline['value']:.3f} tok/s")
+
+    line = {
+        "metric": "decode tok/s (1B bf16, b=1 and b=32) + achieved HBM GB/s vs MI355X peak",
+        "value": tok_s,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,0.02) bf16 weights drawn in HBM, 128 uniform random prompt ids, greedy",
+        "config": {"workload": "C2: 1B-class GQA decoder bf16, batch 1, 128-token prompt, greedy decode",
+                   "vocab": 32000, "d_model": 2048, "layers": 16, "heads": 32, "kv_heads": 8, "head_dim": 64,
+                   "hidden": 5632, "batch": 1, "prompt": 128, "mean_cache_length": b1["mean_len"]},
+        "achieved_GBps": achieved,
+        "frac_of_hbm_peak": achieved / HBM_PEAK_GBPS,
+        "copy_GBps": copy_gbps,
+        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<uint16_t,1,8,DLK_EPI_SWIGLU> (gate/up + SiLU*up)",
+                     "achieved": gate_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gate_gbps / HBM_PEAK_GBPS,
+                     "traffic": None, "bytes_per_launch": gate_bytes, "avg_launch_us": gate_avg_ms * 1e3},
+        "kernels": kernels,
+        "cpu_baseline": baseline,
+    }
+    line.update(extra)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

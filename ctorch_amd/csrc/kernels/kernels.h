@@ -1,0 +1,159 @@
+// Launch entries of the hand-written CDNA4 kernels (gfx950).  Plain C structs of device pointers, sizes and a
+// stream; each entry returns 0 or a HIP error code.  The host C++ layers fill these from tensors.
+#pragma once
+
+#include "backends/hip_backend.h"
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element codes follow dl_dtype */
+enum { DLK_F32 = 0, DLK_F64 = 1, DLK_I64 = 2, DLK_BOOL = 3, DLK_BF16 = 5 };
+
+/* ------------------------------------------------------------------------------------------------------
+ * Projection GEMV over bf16 (or f32) weights, f32 activations and f32 accumulation:
+ *   y[m, n] = epilogue( s_m * sum_k x[m, k] * g[k] * W[n, k] )
+ * with g = the RMSNorm weight and s_m = 1/sqrt(mean_k x[m,k]^2 + eps) when apply_norm (the preceding RMSNorm
+ * fused into this launch), else g = 1, s_m = 1.
+ * Replaces the reference's cast_pair upcast + cuBLAS GEMM of every decoder Linear
+ * (src/ops/matmul.cpp:14-67, src/kernels/cuda/matmul.cpp:9-93) and the RMSNorm/RoPE/KV-append/SiLU/residual
+ * passes around them (src/kernels/cuda/normalization.cu:12-42, pointwise.cu:38-44,147-153,267-281).
+ * ---------------------------------------------------------------------------------------------------- */
+enum {
+    DLK_EPI_STORE = 0,    /* y = acc (+ bias); optionally advances *bump_position by bump_count */
+    DLK_EPI_RESIDUAL = 1, /* y = residual + acc; optionally advances *bump_position by bump_count */
+    DLK_EPI_QKV = 2,      /* segments q|k|v: (+LoRA) RoPE on q,k; q -> y, k,v -> cache at position + l */
+    DLK_EPI_SWIGLU = 3,   /* segments gate|up: y = silu(gate) * up */
+    DLK_EPI_LOGITS = 4    /* y = acc; per-block best (value, index) for greedy / Gumbel-max sampling */
+};
+
+typedef struct dlk_sample_partial {
+    double score;
+    int64_t index;
+} dlk_sample_partial;
+
+typedef struct dlk_gemv_params {
+    const float* x;         /* [M, ldx] f32 */
+    int64_t ldx;
+    int M, K;
+    int nseg;               /* 1..3 weight segments stacked along n */
+    const void* w[3];       /* [seg_rows[i], K] row-major */
+    int seg_rows[3];
+    int w_bf16;
+    int apply_norm;         /* fuse the preceding RMSNorm: scale row m by 1/sqrt(mean(x^2)+eps), weight g */
+    const void* norm_weight; /* RMSNorm weight [K] (f32, or bf16 when norm_bf16); NULL means g = 1 */
+    int norm_bf16;
+    float epsilon;
+    float acc_scale;        /* multiplies the accumulated dot products (1 for a plain projection) */
+    int epilogue;
+    float* y;               /* output rows [M, ldy] (QKV: the q rows) */
+    int64_t ldy;
+    const float* residual;  /* RESIDUAL: [M, ldres] f32 (may alias y) */
+    int64_t ldres;
+    const void* bias;       /* STORE: optional [N] */
+    int bias_bf16;
+    int64_t m_base;         /* global row of x row 0 (QKV position mapping, sample partial rows) */
+    /* QKV */
+    int head_dim, kv_heads, length; /* global row m -> batch m / length, position *position + m % length */
+    const float* cosine;    /* [capacity, head_dim/2] f32 */
+    const float* sine;
+    const int64_t* position;
+    void* k_cache;          /* [B, kv_heads, capacity, head_dim] */
+    void* v_cache;
+    int cache_bf16;
+    int64_t cache_capacity;
+    const float* lora_hidden[3]; /* per segment: [M_total, rank] f32 hidden = down(norm(x)) or NULL */
+    const void* lora_up[3];      /* per segment: [seg_rows, rank] */
+    int lora_rank;
+    float lora_scale;
+    /* STORE / RESIDUAL: device cache length advanced by one thread after the launch's reads of it */
+    int64_t* bump_position;
+    int64_t bump_count;
+    /* LOGITS */
+    int sample_mode;        /* 0: none, 1: greedy, 2: Gumbel-max */
+    double temperature;
+    uint64_t key_seed, key_stream;
+    const int64_t* key_label; /* if set, the key is fold_in(key, *key_label) */
+    dlk_sample_partial* partial; /* [M_total, blocks] */
+    int partial_blocks;
+} dlk_gemv_params;
+
+/* Number of work-groups the launch uses for its n range (the LOGITS partial row length). */
+int dlk_gemv_blocks(const dlk_gemv_params* p);
+int dlk_gemv(const dlk_gemv_params* p, dlh_stream stream);
+
+/* ------------------------------------------------------------------------------------------------------
+ * Split-K GQA decode attention (flash-decoding).  Q rows m = b*L + l of [B*L, H*hd] f32 (post-RoPE);
+ * K/V cache [B, KV, capacity, hd] (bf16 or f32, keys already rotated); first = *position (or first_host);
+ * S = first + L keys; causal: row l sees keys <= first + l.  One work-group per (key split, query-row
+ * block, b, kv head) stages 64-key K/V tiles in LDS and serves all H/KV query heads of that KV head.
+ * Replaces grouped_block + attention_weights (src/ops/attention.cpp:65-95) i.e. two batched cuBLAS GEMMs
+ * and attention_softmax_kernel (src/kernels/cuda/reduction.cu:149-169).
+ * ---------------------------------------------------------------------------------------------------- */
+typedef struct dlk_attention_params {
+    const float* q;
+    int64_t ldq;
+    const void* k;
+    const void* v;
+    int kv_bf16;
+    int64_t capacity;        /* rows per (b, kv head) in the K/V storage */
+    const int64_t* position; /* device length before this chunk, or NULL to use first_host */
+    int64_t first_host;
+    int B, L, H, KV, hd;
+    float scale;
+    int causal;
+    float* out;              /* [B*L, ldo] f32, head h at columns h*hd */
+    int64_t ldo;
+    int splits;              /* key splits; > 1 needs partial buffers */
+    int chunk;               /* keys per split (multiple of the tile) */
+    float* partial_o;        /* [B*H*L, splits, hd] */
+    float* partial_ml;       /* [B*H*L, splits, 2] */
+} dlk_attention_params;
+
+int dlk_attention(const dlk_attention_params* p, dlh_stream stream);
+
+/* ------------------------------------------------------------------------------------------------------
+ * Small kernels of the token loop and the tensor API.
+ * ---------------------------------------------------------------------------------------------------- */
+/* Strided copy with dtype conversion: dst[idx(dst_strides)] = convert(src[idx(src_strides)]), rank <= 8. */
+int dlk_copy(const void* src, int src_dtype, const int64_t* src_strides, void* dst, int dst_dtype,
+             const int64_t* dst_strides, const int64_t* shape, int rank, dlh_stream stream);
+int dlk_fill(void* dst, int dtype, int64_t count, double value, dlh_stream stream);
+/* Embedding rows: out[i, :] = weight[ids[i], :] converted to out_dtype; ids outside [0, V) give a zero row
+ * and set *error_flag (if given) to 1. */
+int dlk_embedding(const int64_t* ids, int64_t count, const void* weight, int weight_dtype, int64_t vocabulary,
+                  int64_t width, void* out, int out_dtype, int32_t* error_flag, dlh_stream stream);
+/* y[r, :] = x[r, :] / sqrt(mean(x^2) + eps) * weight (weight f32 or bf16, may be NULL); f32 in and out. */
+int dlk_rms_norm(const float* x, int64_t rows, int64_t width, const void* weight, int weight_bf16, float epsilon,
+                 float* y, dlh_stream stream);
+/* Interleaved RoPE on contiguous x [outer, L, D] f32 with tables [L, D/2]. */
+int dlk_rope(const float* x, int64_t outer, int64_t length, int64_t dim, const float* cosine, const float* sine,
+             float* y, dlh_stream stream);
+/* First maximum of each row (NaN first); x [rows, n] f32 contiguous -> out i64 [rows]. */
+int dlk_argmax(const float* x, int64_t rows, int64_t n, int64_t* out, dlh_stream stream);
+/* Per-block candidates of a [rows, n] logits matrix (greedy or Gumbel-max), for dlk_sample_finalize. */
+int dlk_sample_partials(const float* logits, int64_t rows, int64_t n, int mode, double temperature,
+                        uint64_t key_seed, uint64_t key_stream, const int64_t* key_label,
+                        dlk_sample_partial* partial, int blocks, dlh_stream stream);
+int dlk_sample_blocks(int64_t n);
+/* Reduces partial [rows, blocks] to ids: out[r] (may be NULL), next_ids[r] (may be NULL), and
+ * tokens[r * token_stride + *step] when tokens != NULL; then advances *step by one if step != NULL. */
+int dlk_sample_finalize(const dlk_sample_partial* partial, int64_t rows, int blocks, int64_t* out,
+                        int64_t* next_ids, int64_t* tokens, int64_t token_stride, int64_t* step,
+                        dlh_stream stream);
+/* Keyed Philox: mode 0 uniform [low, high), mode 1 standard normal times scale; output f32 or bf16. */
+int dlk_random(uint64_t seed, uint64_t stream_bits, int64_t count, int mode, double low, double high,
+               double scale, void* out, int out_dtype, dlh_stream stream);
+/* Plain y = x W^T (+ bias) for shapes the GEMV cannot take (K not a multiple of the 16-byte chunk). */
+int dlk_linear_generic(const float* x, int64_t rows, int64_t K, const void* w, int w_dtype, int64_t N,
+                       const void* bias, int bias_dtype, float* y, dlh_stream stream);
+/* Streaming copy of `bytes` (multiple of 16) for the bandwidth probe. */
+int dlk_stream_copy(const void* src, void* dst, uint64_t bytes, dlh_stream stream);
+
+#ifdef __cplusplus
+}
+#endif

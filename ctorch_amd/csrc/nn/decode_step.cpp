@@ -1,0 +1,235 @@
+// Fused per-layer decode step (see decode_step.h).
+#include "nn/decode_step.h"
+
+#include <cmath>
+#include <stdexcept>
+
+namespace dl::detail {
+
+using nn::KVCache;
+using nn::TransformerDecoderLayer;
+
+DType cache_dtype(const TransformerDecoderLayer& layer) {
+    return layer.attention().query().weight().dtype() == DType::bf16 ? DType::bf16 : DType::f32;
+}
+
+void DecodeWorkspace::ensure(const TransformerDecoderLayer& layer, Index n, Index heads_total, Index hidden_features,
+                             int splits, Device device) {
+    const Index d = layer.attention().dimensions();
+    const Index hd = layer.attention().head_dim();
+    if (!q.defined() || rows < n || q.size(1) != heads_total || activation.size(1) != hidden_features ||
+        !(q.device() == device)) {
+        rows = n;
+        q = empty_tensor({n, heads_total}, DType::f32, device);
+        attention = empty_tensor({n, d}, DType::f32, device);
+        hidden = empty_tensor({n, d}, DType::f32, device);
+        activation = empty_tensor({n, hidden_features}, DType::f32, device);
+        splits_capacity = 0;
+        lora_query = Tensor();
+        lora_value = Tensor();
+    }
+    const Index heads = layer.attention().heads();
+    const Index partial_rows = n * heads; // one partial row per (b, h, l)
+    if (splits > 1 && (splits_capacity < splits || partial_o.size(0) < partial_rows)) {
+        splits_capacity = splits;
+        partial_o = empty_tensor({partial_rows, splits, hd}, DType::f32, device);
+        partial_ml = empty_tensor({partial_rows, splits, 2}, DType::f32, device);
+    }
+    const auto* qa = layer.attention().query_adapter();
+    const auto* va = layer.attention().value_adapter();
+    if (qa && (!lora_query.defined() || lora_query.size(0) < n || lora_query.size(1) != qa->rank()))
+        lora_query = empty_tensor({n, qa->rank()}, DType::f32, device);
+    if (va && (!lora_value.defined() || lora_value.size(0) < n || lora_value.size(1) != va->rank()))
+        lora_value = empty_tensor({n, va->rank()}, DType::f32, device);
+}
+
+namespace {
+const void* norm_data(const nn::RMSNorm& norm, int& bf16) {
+    const auto& w = norm.weight();
+    if (!w) { bf16 = 0; return nullptr; }
+    if (w->dtype() != DType::f32 && w->dtype() != DType::bf16) throw std::invalid_argument("RMSNorm weight dtype");
+    bf16 = w->dtype() == DType::bf16;
+    return w->data<void>();
+}
+
+struct Observe {
+    LaunchObserver* observer;
+    Observe(LaunchObserver* o, const char* name, double bytes) : observer(o) {
+        if (observer) observer->before(name, bytes);
+    }
+    ~Observe() {
+        if (observer) observer->after();
+    }
+};
+} // namespace
+
+void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float* x_out, Index batch, Index length,
+                  KVCache& cache, DecodeWorkspace& ws, int splits, int chunk, GpuContext& context,
+                  LaunchObserver* observer) {
+    const auto& attention = layer.attention();
+    const auto& ff = layer.feedforward();
+    const Index d = attention.dimensions(), H = attention.heads(), KV = attention.kv_heads(), hd = attention.head_dim();
+    const Index F = ff.gate().weight().size(0);
+    const Index rows = batch * length;
+    const Device device = attention.query().weight().device();
+    ws.ensure(layer, rows, H * hd, F, splits, device);
+    if (!cache.reserved()) throw std::logic_error("decode_layer needs a reserved cache");
+    const bool kv_bf16 = cache.key().dtype() == DType::bf16;
+    const double kv_bytes_per = static_cast<double>(batch) * KV * hd * (kv_bf16 ? 2 : 4);
+
+    // 1. LoRA hidden states (down projections of the normalised input), when adapters are attached
+    auto lora_down = [&](const nn::LoRAAdapter* adapter, Tensor& hidden) {
+        if (!adapter) return;
+        int ab = 0, nb = 0;
+        dlk_gemv_params p = gemv_params(x_in, rows, d, DLK_EPI_STORE);
+        p.apply_norm = 1;
+        p.norm_weight = norm_data(layer.attention_norm(), nb);
+        p.norm_bf16 = nb;
+        p.epsilon = static_cast<float>(layer.attention_norm().epsilon());
+        p.nseg = 1;
+        p.w[0] = weight_data(adapter->down().weight(), ab, "LoRA down");
+        p.seg_rows[0] = static_cast<int>(adapter->rank());
+        p.w_bf16 = ab;
+        p.y = static_cast<float*>(mutable_data(hidden));
+        p.ldy = adapter->rank();
+        Observe o(observer, "lora_down", static_cast<double>(adapter->down().weight().numel()) * (ab ? 2 : 4));
+        hip_check(dlk_gemv(&p, context.stream), "LoRA down projection");
+    };
+    lora_down(attention.query_adapter(), ws.lora_query);
+    lora_down(attention.value_adapter(), ws.lora_value);
+
+    // 2. QKV projection: fused RMSNorm prologue, (LoRA,) RoPE and KV append epilogue
+    {
+        int qb = 0, kb = 0, vb = 0, nb = 0;
+        dlk_gemv_params p = gemv_params(x_in, rows, d, DLK_EPI_QKV);
+        p.apply_norm = 1;
+        p.norm_weight = norm_data(layer.attention_norm(), nb);
+        p.norm_bf16 = nb;
+        p.epsilon = static_cast<float>(layer.attention_norm().epsilon());
+        p.nseg = 3;
+        p.w[0] = weight_data(attention.query().weight(), qb, "QKV");
+        p.w[1] = weight_data(attention.key().weight(), kb, "QKV");
+        p.w[2] = weight_data(attention.value().weight(), vb, "QKV");
+        if (qb != kb || qb != vb) throw std::invalid_argument("attention projections must share one dtype");
+        p.seg_rows[0] = static_cast<int>(H * hd);
+        p.seg_rows[1] = p.seg_rows[2] = static_cast<int>(KV * hd);
+        p.w_bf16 = qb;
+        p.y = static_cast<float*>(mutable_data(ws.q));
+        p.ldy = H * hd;
+        p.head_dim = static_cast<int>(hd);
+        p.kv_heads = static_cast<int>(KV);
+        p.length = static_cast<int>(length);
+        p.cosine = attention.rotary().cosine().data<float>();
+        p.sine = attention.rotary().sine().data<float>();
+        p.position = cache.position_data();
+        p.k_cache = cache.key_data();
+        p.v_cache = cache.value_data();
+        p.cache_bf16 = kv_bf16;
+        p.cache_capacity = cache.capacity();
+        if (const auto* a = attention.query_adapter()) {
+            int ub = 0;
+            p.lora_hidden[0] = ws.lora_query.data<float>();
+            p.lora_up[0] = weight_data(a->up().weight(), ub, "LoRA up");
+            p.lora_rank = static_cast<int>(a->rank());
+            p.lora_scale = static_cast<float>(a->scale());
+        }
+        if (const auto* a = attention.value_adapter()) {
+            int ub = 0;
+            p.lora_hidden[2] = ws.lora_value.data<float>();
+            p.lora_up[2] = weight_data(a->up().weight(), ub, "LoRA up");
+            p.lora_rank = static_cast<int>(a->rank());
+            p.lora_scale = static_cast<float>(a->scale());
+        }
+        if (attention.query_adapter() && attention.value_adapter() &&
+            (attention.query_adapter()->rank() != attention.value_adapter()->rank() ||
+             attention.query_adapter()->scale() != attention.value_adapter()->scale()))
+            throw std::invalid_argument("query and value adapters must share rank and alpha");
+        const double bytes = static_cast<double>((H + 2 * KV) * hd * d) * (qb ? 2 : 4) + 2.0 * kv_bytes_per * length;
+        Observe o(observer, "qkv_rope_append", bytes);
+        hip_check(dlk_gemv(&p, context.stream), "QKV projection");
+    }
+
+    // 3. split-K attention over the cache (reads the device length, sees the keys just appended)
+    {
+        dlk_attention_params a{};
+        a.q = ws.q.data<float>();
+        a.ldq = H * hd;
+        a.k = cache.key_data();
+        a.v = cache.value_data();
+        a.kv_bf16 = kv_bf16;
+        a.capacity = cache.capacity();
+        a.position = cache.position_data();
+        a.B = static_cast<int>(batch); a.L = static_cast<int>(length); a.H = static_cast<int>(H);
+        a.KV = static_cast<int>(KV); a.hd = static_cast<int>(hd);
+        a.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(hd)));
+        a.causal = 1;
+        a.out = static_cast<float*>(mutable_data(ws.attention));
+        a.ldo = d;
+        a.splits = splits;
+        a.chunk = chunk;
+        if (splits > 1) {
+            a.partial_o = static_cast<float*>(mutable_data(ws.partial_o));
+            a.partial_ml = static_cast<float*>(mutable_data(ws.partial_ml));
+        }
+        const double bytes = 2.0 * kv_bytes_per * static_cast<double>(cache.length() + length);
+        Observe o(observer, "attention", bytes);
+        hip_check(dlk_attention(&a, context.stream), "attention");
+    }
+
+    // 4. output projection + residual; advances the device cache length by `length`
+    {
+        int ob = 0;
+        dlk_gemv_params p = gemv_params(ws.attention.data<float>(), rows, d, DLK_EPI_RESIDUAL);
+        p.nseg = 1;
+        p.w[0] = weight_data(attention.output().weight(), ob, "output projection");
+        p.seg_rows[0] = static_cast<int>(d);
+        p.w_bf16 = ob;
+        p.y = static_cast<float*>(mutable_data(ws.hidden));
+        p.ldy = d;
+        p.residual = x_in;
+        p.ldres = d;
+        p.bump_position = cache.position_data();
+        p.bump_count = length;
+        Observe o(observer, "output_residual", static_cast<double>(d * d) * (ob ? 2 : 4));
+        hip_check(dlk_gemv(&p, context.stream), "output projection");
+    }
+
+    // 5. gate/up projection: fused RMSNorm prologue and SiLU(gate) * up epilogue
+    {
+        int gb = 0, ub = 0, nb = 0;
+        dlk_gemv_params p = gemv_params(ws.hidden.data<float>(), rows, d, DLK_EPI_SWIGLU);
+        p.apply_norm = 1;
+        p.norm_weight = norm_data(layer.feedforward_norm(), nb);
+        p.norm_bf16 = nb;
+        p.epsilon = static_cast<float>(layer.feedforward_norm().epsilon());
+        p.nseg = 2;
+        p.w[0] = weight_data(ff.gate().weight(), gb, "gate");
+        p.w[1] = weight_data(ff.up().weight(), ub, "up");
+        if (gb != ub) throw std::invalid_argument("gate and up projections must share one dtype");
+        p.seg_rows[0] = p.seg_rows[1] = static_cast<int>(F);
+        p.w_bf16 = gb;
+        p.y = static_cast<float*>(mutable_data(ws.activation));
+        p.ldy = F;
+        Observe o(observer, "gate_up_silu", static_cast<double>(2 * F * d) * (gb ? 2 : 4));
+        hip_check(dlk_gemv(&p, context.stream), "gate/up projection");
+    }
+
+    // 6. down projection + residual
+    {
+        int db = 0;
+        dlk_gemv_params p = gemv_params(ws.activation.data<float>(), rows, F, DLK_EPI_RESIDUAL);
+        p.nseg = 1;
+        p.w[0] = weight_data(ff.down().weight(), db, "down");
+        p.seg_rows[0] = static_cast<int>(d);
+        p.w_bf16 = db;
+        p.y = x_out;
+        p.ldy = d;
+        p.residual = ws.hidden.data<float>();
+        p.ldres = d;
+        Observe o(observer, "down_residual", static_cast<double>(F * d) * (db ? 2 : 4));
+        hip_check(dlk_gemv(&p, context.stream), "down projection");
+    }
+    cache.advance(length);
+}
+
+} // namespace dl::detail

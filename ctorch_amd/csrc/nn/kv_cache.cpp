@@ -1,0 +1,91 @@
+// KV cache (reference src/nn/kv_cache.cpp:9-42).  Storage [.., capacity, D] is allocated by the first append (or
+// by the fused decode path's reserve), appends copy along the second-to-last axis, key()/value() are narrow views
+// and clear/truncate only move the length.  On a GPU the length is mirrored in an i64 device word that the
+// fused kernels read (RoPE position, KV slot, attention length) and advance, so that a captured step needs no
+// host-side arguments.
+#include "nn/ops_internal.h"
+
+#include <stdexcept>
+
+namespace dl::nn {
+
+using namespace dl::detail;
+
+KVCache::KVCache(Index capacity) : capacity_(capacity) {
+    if (capacity <= 0) throw std::invalid_argument("KV cache capacity must be positive");
+}
+
+void KVCache::sync_position() const {
+    if (!position_) return;
+    auto& context = gpu_context(position_->device().index);
+    hip_check(dlk_fill(mutable_data(*position_), DLK_I64, 1, static_cast<double>(length_), context.stream),
+              "KV cache length");
+}
+
+void KVCache::reserve(Index batch, Index heads, Index head_dim, DType dtype, Device device) {
+    const Shape shape{batch, heads, capacity_, head_dim};
+    if (key_) {
+        if (key_->shape() != shape || key_->dtype() != dtype || !(key_->device() == device))
+            throw std::invalid_argument("KV cache shape, dtype or device changed");
+        return;
+    }
+    key_ = empty_tensor(shape, dtype, device);
+    value_ = empty_tensor(shape, dtype, device);
+    if (device.type == DeviceType::gpu) {
+        position_ = empty_tensor({1}, DType::i64, device);
+        sync_position();
+    }
+}
+
+void KVCache::append(const Tensor& key, const Tensor& value) {
+    if (key.ndim() < 2 || value.ndim() != key.ndim()) throw std::invalid_argument("KV cache append needs [.., n, D]");
+    const auto count = key.size(-2);
+    if (count != value.size(-2) || count > capacity_ - length_)
+        throw std::invalid_argument("KV cache append exceeds capacity or has unequal key/value lengths");
+    if (!key_) {
+        Shape shape = key.shape();
+        shape[shape.size() - 2] = capacity_;
+        key_ = empty_tensor(shape, key.dtype(), key.device());
+        value_ = empty_tensor(shape, key.dtype(), key.device());
+        if (key.device().type == DeviceType::gpu) position_ = empty_tensor({1}, DType::i64, key.device());
+    } else {
+        Shape shape = key.shape();
+        shape[shape.size() - 2] = capacity_;
+        if (key_->shape() != shape || !(key_->device() == key.device()))
+            throw std::invalid_argument("KV cache shape, dtype or device changed");
+    }
+    // values are stored in the cache's dtype (bf16 storage for bf16 models)
+    copy_into(key_->narrow(-2, length_, count), key.to(key_->device()));
+    copy_into(value_->narrow(-2, length_, count), value.to(value_->device()));
+    length_ += count;
+    sync_position();
+}
+
+Tensor KVCache::key() const {
+    if (!key_) throw std::logic_error("KV cache has no key tensor before its first append");
+    return key_->narrow(-2, 0, length_);
+}
+
+Tensor KVCache::value() const {
+    if (!value_) throw std::logic_error("KV cache has no value tensor before its first append");
+    return value_->narrow(-2, 0, length_);
+}
+
+void KVCache::clear() {
+    length_ = 0;
+    sync_position();
+}
+
+void KVCache::truncate(Index length) {
+    if (length < 0 || length > length_) throw std::out_of_range("KV cache truncation must keep an existing prefix");
+    length_ = length;
+    sync_position();
+}
+
+void* KVCache::key_data() const { return key_ ? mutable_data(*key_) : nullptr; }
+void* KVCache::value_data() const { return value_ ? mutable_data(*value_) : nullptr; }
+std::int64_t* KVCache::position_data() const {
+    return position_ ? static_cast<std::int64_t*>(mutable_data(*position_)) : nullptr;
+}
+
+} // namespace dl::nn

@@ -1,0 +1,67 @@
+#ifndef CTORCH_DECODER_C_API_H
+#define CTORCH_DECODER_C_API_H
+/*
+ * Decoder C17 surface: every entry of the reference's include/dl/decoder_c_api.h:13-41 (same names and
+ * arguments; bodies in ctorch_amd/csrc/api/decoder.cpp), plus two additive extensions marked below.
+ * The cache handle belongs to one inference request, holds one K/V store per layer and is released
+ * independently of the model.
+ */
+#include "dl/c_api.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct dl_decoder_cache dl_decoder_cache;
+
+/* decoder_c_api.h:15-20 */
+DL_API dl_status dl_tensordot(const dl_tensor* a, const dl_tensor* b,
+    dl_shape axes_a, dl_shape axes_b, dl_tensor** output);
+DL_API dl_status dl_rotary_embedding(const dl_tensor* input, const dl_tensor* cosine,
+    const dl_tensor* sine, dl_tensor** output);
+DL_API dl_status dl_grouped_query_attention(const dl_tensor* query, const dl_tensor* key,
+    const dl_tensor* value, const dl_tensor* keep_mask, dl_tensor** output);
+
+/* decoder_c_api.h:22-35 */
+DL_API dl_status dl_swiglu_create(int64_t dimensions, int64_t hidden, int32_t bias,
+    dl_tensor_options options, dl_module** output);
+DL_API dl_status dl_lora_linear_create(const dl_module* base, int64_t rank, double alpha, dl_module** output);
+DL_API dl_status dl_lora_linear_merge(const dl_module* adapter, dl_module** output);
+DL_API dl_status dl_rotary_embedding_create(int64_t dimensions, int64_t capacity, double base,
+    dl_tensor_options options, dl_module** output);
+DL_API dl_status dl_rotary_embedding_forward(dl_module* rotary, const dl_tensor* input,
+    int64_t offset, dl_tensor** output);
+DL_API dl_status dl_grouped_query_attention_create(int64_t dimensions, int64_t heads, int64_t kv_heads,
+    int64_t context, dl_tensor_options options, dl_module** output);
+DL_API dl_status dl_transformer_decoder_create(int64_t layers, int64_t dimensions, int64_t heads,
+    int64_t kv_heads, int64_t hidden, int64_t context, dl_tensor_options options, dl_module** output);
+
+/* decoder_c_api.h:37-42 */
+DL_API dl_status dl_decoder_cache_create(const dl_module* decoder, dl_decoder_cache** output);
+DL_API void dl_decoder_cache_release(dl_decoder_cache* cache);
+DL_API dl_status dl_decoder_cache_clear(dl_decoder_cache* cache);
+DL_API dl_status dl_decoder_cache_truncate(dl_decoder_cache* cache, int64_t length);
+DL_API dl_status dl_decoder_cache_length(const dl_decoder_cache* cache, int64_t* length);
+DL_API dl_status dl_transformer_decoder_decode(dl_module* decoder, const dl_tensor* input,
+    dl_decoder_cache* cache, dl_tensor** output);
+
+/* Extension (no reference counterpart): the same constructor with the RoPE base the reference hard-codes
+ * to 10000 (src/nn/decoder.cpp:70), needed by base-500000 models. */
+DL_API dl_status dl_transformer_decoder_create_with_base(int64_t layers, int64_t dimensions, int64_t heads,
+    int64_t kv_heads, int64_t hidden, int64_t context, double rope_base, dl_tensor_options options,
+    dl_module** output);
+/* Extension (no reference counterpart): attaches unmerged rank-`rank` LoRA adapters (scale alpha/rank,
+ * `up` zero-initialised) to the query and/or value projection of every layer; they appear in the state as
+ * layer{i}.attention.{query,value}_adapter.{down,up}.weight. */
+DL_API dl_status dl_transformer_decoder_attach_lora(dl_module* decoder, int64_t rank, double alpha,
+    int32_t query, int32_t value);
+/* Extension: writes the K and V of one layer's cache directly (keys already rotated), the reference's
+ * KVCache::append route (include/dl/decoder.h:52) for seeding a prefix.  key/value are [B, KV, n, D]. */
+DL_API dl_status dl_decoder_cache_append(dl_decoder_cache* cache, int64_t layer, const dl_tensor* key,
+    const dl_tensor* value);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

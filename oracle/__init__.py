@@ -279,8 +279,8 @@ def parameter_names(cfg: ModelConfig) -> list[tuple[str, tuple[int, ...]]]:
                   (p + "attention.value.weight", (KV * hd, d)), (p + "attention.output.weight", (d, H * hd))]
         if cfg.lora_rank:
             r = cfg.lora_rank
-            names += [(p + "attention.query.lora.down.weight", (r, d)), (p + "attention.query.lora.up.weight", (H * hd, r)),
-                      (p + "attention.value.lora.down.weight", (r, d)), (p + "attention.value.lora.up.weight", (KV * hd, r))]
+            names += [(p + "attention.query_adapter.down.weight", (r, d)), (p + "attention.query_adapter.up.weight", (H * hd, r)),
+                      (p + "attention.value_adapter.down.weight", (r, d)), (p + "attention.value_adapter.up.weight", (KV * hd, r))]
         names += [(p + "feedforward.gate.weight", (F, d)), (p + "feedforward.up.weight", (F, d)),
                   (p + "feedforward.down.weight", (d, F)), (p + "attention_norm.weight", (d,)),
                   (p + "feedforward_norm.weight", (d,))]
@@ -290,14 +290,15 @@ def parameter_names(cfg: ModelConfig) -> list[tuple[str, tuple[int, ...]]]:
 
 def synthesize_weights(cfg: ModelConfig, root=(1234, 0), scale: float = 0.02) -> dict[str, np.ndarray]:
     """Seeded weights: slot s draws 0.02*randn(fold_in(root, s)) (RNE to bf16 for bf16 models).
-    Norm weights keep their module default of ones; LoRA up (B) draws 1e-3*randn."""
+    Norm weights keep their module default of ones; LoRA up (B) draws 1e-3*randn.  Adapter names follow the product's extension
+    (``attention.{query,value}_adapter.{down,up}.weight``)."""
     dtype = BF16 if cfg.dtype == "bf16" else F32
     out = {}
     for slot, (name, shape) in enumerate(parameter_names(cfg)):
         if name.endswith("norm.weight") or name == "decoder.normalization.weight":
             out[name] = np.ones(shape, np.float32)
             continue
-        s = 1e-3 if name.endswith("lora.up.weight") else scale
+        s = 1e-3 if name.endswith("_adapter.up.weight") else scale
         out[name] = normal_weights(fold_in(root, slot), shape, s, dtype)
     return out
 
@@ -330,10 +331,10 @@ class OracleLM:
                 setattr(L, f, _ptr(self.w[p + f + ".weight"]))
             L.cosine, L.sine = _ptr(self.tables[i][0]), _ptr(self.tables[i][1])
             if cfg.lora_rank:
-                L.query_down = _ptr(self.w[p + "attention.query.lora.down.weight"])
-                L.query_up = _ptr(self.w[p + "attention.query.lora.up.weight"])
-                L.value_down = _ptr(self.w[p + "attention.value.lora.down.weight"])
-                L.value_up = _ptr(self.w[p + "attention.value.lora.up.weight"])
+                L.query_down = _ptr(self.w[p + "attention.query_adapter.down.weight"])
+                L.query_up = _ptr(self.w[p + "attention.query_adapter.up.weight"])
+                L.value_down = _ptr(self.w[p + "attention.value_adapter.down.weight"])
+                L.value_up = _ptr(self.w[p + "attention.value_adapter.up.weight"])
         self.w["decoder.normalization.weight"] = np.ascontiguousarray(self.w["decoder.normalization.weight"], np.float32)
         self.model = Model()
         self.model.config = Config(cfg.vocab, cfg.layers, cfg.dimensions, cfg.heads, cfg.kv_heads, cfg.hidden,

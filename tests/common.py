@@ -1,0 +1,55 @@
+"""Shared test helpers: one seeded model evaluated by the CPU oracle (the checker) and by the GPU library.
+
+The oracle's synthetic weights (tests' and bench's common definition, oracle.synthesize_weights) are loaded
+into the library's modules through the C ABI: Embedding from tokens.weight, TransformerDecoder from the
+decoder.* entries (its RoPE buffers stay the library's own), Linear head from output.weight.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import ctorch_amd as ct
+import oracle
+
+
+class GpuLM:
+    def __init__(self, cfg: oracle.ModelConfig, weights: dict[str, np.ndarray]):
+        dtype = ct.BF16 if cfg.dtype == "bf16" else ct.F32
+        gpu = ct.device("gpu")
+        self.cfg = cfg
+        self.decoder = ct.transformer_decoder(cfg.layers, cfg.dimensions, cfg.heads, cfg.kv_heads, cfg.hidden,
+                                              cfg.context, dtype, gpu, cfg.rope_base)
+        if cfg.lora_rank:
+            ct.check(ct.lib().dl_transformer_decoder_attach_lora(self.decoder.handle, cfg.lora_rank, cfg.lora_alpha,
+                                                                 1, 1))
+        state = {}
+        for name, value in weights.items():
+            if name.startswith("decoder."):
+                state[name[len("decoder."):]] = value
+        current = self.decoder.state()
+        for name, tensor in current.items():
+            state.setdefault(name, tensor)
+        dtypes = {n: (ct.BF16 if v.dtype == np.uint16 else None) for n, v in state.items() if isinstance(v, np.ndarray)}
+        self.decoder.load_state(state, dtypes)
+        self.embedding = ct.embedding_from(ct.Tensor.from_numpy(weights["tokens.weight"], dtype, gpu))
+        self.head = ct.linear_from(ct.Tensor.from_numpy(weights["output.weight"], dtype, gpu))
+        self.lm = ct.DecoderLM(self.embedding, self.decoder, self.head)
+
+    def cache(self) -> ct.DecoderCache:
+        return ct.DecoderCache(self.decoder)
+
+    def generate(self, prompt, steps, temperature=0.0, key=(0, 0), use_graph=True, cache=None):
+        return self.lm.generate(prompt, cache or self.cache(), steps, temperature, key, use_graph)
+
+    def logits(self, ids, cache):
+        return self.lm.logits(ids, cache)
+
+
+def build_pair(cfg: oracle.ModelConfig, root=(1234, 0), scale: float = 0.02, weights=None):
+    weights = weights if weights is not None else oracle.synthesize_weights(cfg, root, scale)
+    return oracle.OracleLM(cfg, weights), GpuLM(cfg, weights)
+
+
+def rel_err(got: np.ndarray, want: np.ndarray) -> float:
+    """max |got - want| / max |want| over the whole array (the f32 logit criterion)."""
+    return float(np.max(np.abs(got.astype(np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))

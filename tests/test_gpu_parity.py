@@ -1,0 +1,205 @@
+"""GPU parity of the decoder token loop against the CPU oracle, through the C ABI.
+
+Tolerances:
+  f32 configs   logits max|d| / max|ref| <= 1e-4 per compared tensor, greedy ids identical;
+  bf16 configs  logits max-abs <= 2e-2 (bf16 weights and KV, f32 accumulation);
+  sampling      ids bit-identical given identical logits and key.
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import ctorch_amd as ct
+import oracle
+from common import GpuLM, build_pair, rel_err
+
+pytestmark = pytest.mark.gpu
+GPU = ct.device("gpu")
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _threads():
+    oracle.lib()
+    oracle.set_threads(16)
+
+
+# ------------------------------------------------------------------------------------------ C1 (f32)
+C1 = oracle.ModelConfig(vocab=256, layers=4, dimensions=256, heads=8, kv_heads=2, hidden=688, context=160, dtype="f32")
+
+
+def test_c1_greedy_128_tokens_identical_and_logits_within_1e4():
+    say("case: C1 tiny f32, 32-byte prompt, 128 greedy tokens")
+    ref, gpu = build_pair(C1, root=(101, 0))
+    prompt = oracle.random_ids((202, 0), 32, 256).reshape(1, 32)
+    want_tokens, want_last = ref.generate(prompt, 128)
+    got_tokens, got_last = gpu.generate(prompt, 128, use_graph=True)
+    assert np.array_equal(got_tokens, want_tokens)
+    assert rel_err(got_last, want_last) <= 1e-4
+    eager_tokens, eager_last = gpu.generate(prompt, 128, use_graph=False)
+    assert np.array_equal(eager_tokens, got_tokens)
+    assert np.array_equal(eager_last, got_last)  # graph replay is the eager step, bit for bit
+
+
+def test_c1_stepwise_logits_and_cache_lengths():
+    say("case: C1 stepwise logits through lm_logits")
+    ref, gpu = build_pair(C1, root=(103, 0))
+    ids = oracle.random_ids((204, 0), 2 * 12, 256).reshape(2, 12)
+    rc, gc = ref.make_cache(2), gpu.cache()
+    for chunk in (ids[:, :5], ids[:, 5:6], ids[:, 6:7], ids[:, 7:12]):
+        want = ref.logits(chunk, rc)[:, -1]
+        got = gpu.logits(chunk, gc)
+        assert rel_err(got, want) <= 1e-4
+        assert gc.length == rc.length
+
+
+def test_decoder_api_chunked_equals_full_and_capacity_rollback():
+    say("case: dl_transformer_decoder_decode chunked vs full, capacity error")
+    cfg = oracle.ModelConfig(vocab=64, layers=2, dimensions=64, heads=4, kv_heads=2, hidden=96, context=16, dtype="f32")
+    ref, gpu = build_pair(cfg, root=(17, 0), scale=0.2)
+    x = np.random.default_rng(10).standard_normal((2, 6, 64)).astype(np.float32)
+    want = ref.decode(x, ref.make_cache(2))
+    cache = gpu.cache()
+    a = ct.decode(gpu.decoder, ct.Tensor.from_numpy(x[:, :2], ct.F32, GPU), cache).numpy()
+    b = ct.decode(gpu.decoder, ct.Tensor.from_numpy(x[:, 2:], ct.F32, GPU), cache).numpy()
+    full = ct.decode(gpu.decoder, ct.Tensor.from_numpy(x, ct.F32, GPU), gpu.cache()).numpy()
+    assert cache.length == 6
+    assert rel_err(np.concatenate([a, b], 1), want) <= 1e-5
+    assert np.max(np.abs(np.concatenate([a, b], 1) - full)) <= 1e-5
+    cache.truncate(2)
+    assert cache.length == 2
+    again = ct.decode(gpu.decoder, ct.Tensor.from_numpy(x[:, 2:], ct.F32, GPU), cache).numpy()
+    assert np.max(np.abs(again - b)) <= 1e-6
+    # a chunk that exceeds the capacity fails and leaves every layer at the prefix
+    with pytest.raises(ct.DLError, match="capacity"):
+        ct.decode(gpu.decoder, ct.Tensor.from_numpy(np.ones((2, 11, 64), np.float32), ct.F32, GPU), cache)
+    assert cache.length == 6
+
+
+# ------------------------------------------------------------------------------------------ bf16
+def test_bf16_model_logits_within_2e2_and_graph_equals_eager():
+    say("case: bf16 2-layer d=512 model, prompt 20 + 24 greedy steps")
+    cfg = oracle.ModelConfig(vocab=1000, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=1376, context=64,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(31, 0), scale=0.05)
+    prompt = oracle.random_ids((32, 0), 3 * 20, cfg.vocab).reshape(3, 20)
+    rc, gc = ref.make_cache(3), gpu.cache()
+    want = ref.logits(prompt, rc)[:, -1]
+    got = gpu.logits(prompt, gc)
+    assert np.max(np.abs(got - want)) <= 2e-2
+    t1, l1 = gpu.generate(prompt, 24, 1.0, (5, 6), use_graph=True)
+    t2, l2 = gpu.generate(prompt, 24, 1.0, (5, 6), use_graph=False)
+    assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
+    # the last sampled id is the oracle's Gumbel-max draw on the same logits and key
+    key = oracle.fold_in((5, 6), 23)
+    assert np.array_equal(oracle.sample(l1, 1.0, key), t1[:, -1])
+
+
+def test_sampler_is_bit_exact_against_the_oracle():
+    say("case: dl_sample greedy and Gumbel-max, ties and NaN rows")
+    rng = np.random.default_rng(4)
+    logits = (rng.standard_normal((6, 32000)) * 3).astype(np.float32)
+    logits[1, 100:110] = 50.0          # ties: the first index wins
+    logits[2, 7] = np.nan               # NaN wins
+    logits[3] = np.round(logits[3])     # many ties under noise
+    t = ct.Tensor.from_numpy(logits, ct.F32, GPU)
+    for temperature, key in ((0.0, (0, 0)), (1.0, (11, 12)), (0.7, (2**63 + 5, 3)), (1e-3, (9, 9))):
+        out = ct.Tensor(ct._new(ct.lib().dl_sample, t.handle, temperature, ct.RandomKey(*key))).numpy()
+        assert np.array_equal(out, oracle.sample(logits, temperature, key)), (temperature, key)
+    greedy = ct.Tensor(ct._new(ct.lib().dl_argmax, t.handle, 1, 0)).numpy()
+    assert np.array_equal(greedy, [oracle.argmax_row(r) for r in logits])
+
+
+# ------------------------------------------------------------------------------------------ operators
+def test_operators_match_the_oracle():
+    say("case: dl_linear / dl_rms_norm / dl_embedding / dl_rotary_embedding / dl_grouped_query_attention")
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((5, 2048)).astype(np.float32)
+    w = (rng.standard_normal((300, 2048)) * 0.02).astype(np.float32)
+    wb = oracle.bf16_encode(w)
+    for weight, dtype in ((w, ct.F32), (wb, ct.BF16)):
+        y = ct.Tensor(ct._new(ct.lib().dl_linear, ct.Tensor.from_numpy(x, ct.F32, GPU).handle,
+                              ct.Tensor.from_numpy(weight, dtype, GPU).handle, None)).numpy()
+        assert rel_err(y, oracle.linear(x, weight)) <= 1e-5
+    # K not a multiple of the vector chunk takes the generic kernel
+    xs = rng.standard_normal((3, 13)).astype(np.float32)
+    ws = rng.standard_normal((7, 13)).astype(np.float32)
+    y = ct.Tensor(ct._new(ct.lib().dl_linear, ct.Tensor.from_numpy(xs, ct.F32, GPU).handle,
+                          ct.Tensor.from_numpy(ws, ct.F32, GPU).handle, None)).numpy()
+    assert rel_err(y, oracle.linear(xs, ws)) <= 1e-5
+    g = rng.standard_normal(2048).astype(np.float32)
+    eps = C.c_double(1e-5)
+    y = ct.Tensor(ct._new(ct.lib().dl_rms_norm, ct.Tensor.from_numpy(x, ct.F32, GPU).handle, ct._shape([2048]),
+                          ct.Tensor.from_numpy(g, ct.F32, GPU).handle, C.byref(eps))).numpy()
+    assert rel_err(y, oracle.rms_norm(x, g, 1e-5)) <= 1e-5
+    table = oracle.bf16_encode(rng.standard_normal((50, 64)).astype(np.float32))
+    ids = np.array([[3, 49, 0], [7, 7, 12]], np.int64)
+    e = ct.Tensor(ct._new(ct.lib().dl_embedding, ct.Tensor.from_numpy(ids, ct.I64, GPU).handle,
+                          ct.Tensor.from_numpy(table, ct.BF16, GPU).handle))
+    assert e.dtype == ct.BF16 and np.array_equal(e.numpy(), table[ids])
+    bad = ct.Tensor.from_numpy(np.array([50], np.int64), ct.I64, GPU)
+    out = C.c_void_p()
+    assert ct.lib().dl_embedding(bad.handle, ct.Tensor.from_numpy(table, ct.BF16, GPU).handle, C.byref(out)) == 1
+    assert "out of range" in ct.last_error()
+    c, s = oracle.rope_tables(64, 9)
+    q = rng.standard_normal((2, 3, 9, 64)).astype(np.float32)
+    y = ct.Tensor(ct._new(ct.lib().dl_rotary_embedding, ct.Tensor.from_numpy(q, ct.F32, GPU).handle,
+                          ct.Tensor.from_numpy(c, ct.F32, GPU).handle, ct.Tensor.from_numpy(s, ct.F32, GPU).handle))
+    want = oracle.rope(q.transpose(0, 2, 1, 3).reshape(18, 3, 64), c, s, np.repeat(np.arange(9)[None], 2, 0).reshape(-1))
+    assert np.max(np.abs(y.numpy() - want.reshape(2, 9, 3, 64).transpose(0, 2, 1, 3))) <= 1e-6
+    for L, S in ((1, 200), (3, 70)):
+        qq = rng.standard_normal((2, 8, L, 64)).astype(np.float32)
+        kk = rng.standard_normal((2, 2, S, 64)).astype(np.float32)
+        vv = rng.standard_normal((2, 2, S, 64)).astype(np.float32)
+        y = ct.Tensor(ct._new(ct.lib().dl_grouped_query_attention, ct.Tensor.from_numpy(qq, ct.F32, GPU).handle,
+                              ct.Tensor.from_numpy(kk, ct.F32, GPU).handle, ct.Tensor.from_numpy(vv, ct.F32, GPU).handle,
+                              None)).numpy()
+        assert np.max(np.abs(y - oracle.attention(qq, kk, vv, -1))) <= 1e-5
+
+
+# ------------------------------------------------------------------------------------------ seeded prefix
+def test_batched_decode_over_a_seeded_prefix():
+    say("case: B=4 decode over a 150-token seeded K/V prefix (the C3 route at small scale)")
+    cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=256, heads=8, kv_heads=2, hidden=512, context=200,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(41, 0), scale=0.05)
+    B, P, hd = 4, 150, cfg.head_dim
+    rc, gc = ref.make_cache(B), gpu.cache()
+    for layer in range(cfg.layers):
+        k = oracle.randn(oracle.fold_in((77, 0), 2 * layer), B * 2 * P * hd).reshape(B, 2, P, hd)
+        v = oracle.randn(oracle.fold_in((77, 0), 2 * layer + 1), B * 2 * P * hd).reshape(B, 2, P, hd)
+        kb, vb = oracle.bf16_encode(k), oracle.bf16_encode(v)
+        gc.append(layer, ct.Tensor.from_numpy(kb, ct.BF16, GPU), ct.Tensor.from_numpy(vb, ct.BF16, GPU))
+        rc.fill(layer, P, oracle.bf16_decode(kb), oracle.bf16_decode(vb))
+    assert gc.length == P
+    ids = oracle.random_ids((78, 0), B, cfg.vocab).reshape(B, 1)
+    for step in range(3):
+        want = ref.logits(ids, rc)[:, -1]
+        got = gpu.logits(ids, gc)
+        assert np.max(np.abs(got - want)) <= 2e-2, step
+        ids = want.argmax(-1).reshape(B, 1)
+
+
+# ------------------------------------------------------------------------------------------ C2 shape
+def test_c2_1b_shape_bf16_decode_parity():
+    say("case: C2 1B bf16 shape (16 layers, d=2048, 32/8 heads, F=5632, V=32000), prompt 8 + 4 steps")
+    cfg = oracle.ModelConfig(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632, context=64,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(2024, 1))
+    prompt = oracle.random_ids((2025, 0), 8, cfg.vocab).reshape(1, 8)
+    got_tokens, got_last = gpu.generate(prompt, 4)
+    # teacher-forced oracle on the GPU's own history: bf16 parity is a logit tolerance, not an id identity
+    history = np.concatenate([prompt, got_tokens[:, :-1]], 1)
+    want = ref.logits(history, ref.make_cache(1))[0]
+    assert np.max(np.abs(got_last[0] - want[-1])) <= 2e-2
+    for step in range(4):  # each greedy id is a maximum of the oracle's logits up to the tolerance
+        row = want[prompt.shape[1] - 1 + step]
+        assert row[got_tokens[0, step]] >= row.max() - 4e-2
+    sampled, logits = gpu.generate(prompt, 3, 1.0, (99, 1))
+    assert np.array_equal(oracle.sample(logits, 1.0, oracle.fold_in((99, 1), 2)), sampled[:, -1])

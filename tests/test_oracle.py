@@ -363,21 +363,21 @@ def test_lora_adapter_equals_merged_weight():
     cfg = _tiny("f32", layers=1, lora=4)
     w = oracle.synthesize_weights(cfg, (31, 0), scale=0.2)
     for n in list(w):
-        if n.endswith("lora.up.weight"):
+        if n.endswith("_adapter.up.weight"):
             w[n] = (w[n] * 200).astype(np.float32)  # make the adapter contribution visible
     lm = oracle.OracleLM(cfg, w)
     merged = dict(w)
     scale = cfg.lora_alpha / cfg.lora_rank
     for proj in ("query", "value"):
         p = f"decoder.layer0.attention.{proj}"
-        B = w[p + ".lora.up.weight"].astype(np.float64)
-        A = w[p + ".lora.down.weight"].astype(np.float64)
+        B = w[f"decoder.layer0.attention.{proj}_adapter.up.weight"].astype(np.float64)
+        A = w[f"decoder.layer0.attention.{proj}_adapter.down.weight"].astype(np.float64)
         merged[p + ".weight"] = (w[p + ".weight"] + scale * (B @ A)).astype(np.float32)
     plain_cfg = _tiny("f32", layers=1)
-    plain = oracle.OracleLM(plain_cfg, {k: v for k, v in merged.items() if "lora" not in k})
+    plain = oracle.OracleLM(plain_cfg, {k: v for k, v in merged.items() if "_adapter" not in k})
     ids = oracle.random_ids((9, 0), 7, cfg.vocab).reshape(1, 7)
     a = lm.logits(ids, lm.make_cache(1))
     b = plain.logits(ids, plain.make_cache(1))
     assert np.max(np.abs(a - b)) < 1e-5
-    base = oracle.OracleLM(plain_cfg, {k: v for k, v in w.items() if "lora" not in k})
+    base = oracle.OracleLM(plain_cfg, {k: v for k, v in w.items() if "_adapter" not in k})
     assert np.max(np.abs(a - base.logits(ids, base.make_cache(1)))) > 1e-3  # the adapter is not a no-op
