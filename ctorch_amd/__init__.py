@@ -422,3 +422,37 @@ def copy_bandwidth(nbytes: int, iterations: int = 20, index: int = 0) -> float:
     gbps = C.c_double()
     check(lib().dl_gpu_copy_bandwidth(index, nbytes, iterations, C.byref(gbps)))
     return gbps.value
+
+
+# ---------------------------------------------------------------------------------------------- operators
+# Each wrapper holds its Tensor arguments for the duration of the call (a bare `.handle` of a temporary would
+# be released by the wrapper's destructor before the library reads it).
+def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    return Tensor(_new(lib().dl_linear, x.handle, weight.handle, bias.handle if bias is not None else None))
+
+
+def rms_norm(x: Tensor, normalized_shape, weight: Tensor | None = None, epsilon: float | None = None) -> Tensor:
+    eps = C.c_double(epsilon) if epsilon is not None else None
+    return Tensor(_new(lib().dl_rms_norm, x.handle, _shape(normalized_shape),
+                       weight.handle if weight is not None else None, C.byref(eps) if eps is not None else None))
+
+
+def embedding(ids: Tensor, weight: Tensor) -> Tensor:
+    return Tensor(_new(lib().dl_embedding, ids.handle, weight.handle))
+
+
+def argmax(x: Tensor, axis: int, keepdim: bool = False) -> Tensor:
+    return Tensor(_new(lib().dl_argmax, x.handle, axis, int(keepdim)))
+
+
+def sample(logits: Tensor, temperature: float, key) -> Tensor:
+    return Tensor(_new(lib().dl_sample, logits.handle, temperature, RandomKey(*key)))
+
+
+def rotary_embedding(x: Tensor, cosine: Tensor, sine: Tensor) -> Tensor:
+    return Tensor(_new(lib().dl_rotary_embedding, x.handle, cosine.handle, sine.handle))
+
+
+def grouped_query_attention(q: Tensor, k: Tensor, v: Tensor, keep_mask: Tensor | None = None) -> Tensor:
+    return Tensor(_new(lib().dl_grouped_query_attention, q.handle, k.handle, v.handle,
+                       keep_mask.handle if keep_mask is not None else None))

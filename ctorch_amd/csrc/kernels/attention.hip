@@ -256,6 +256,7 @@ extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stre
         return static_cast<int>(hipErrorInvalidValue);
     if (p.kv_bf16) {
         switch (p.hd) {
+        case 16: return dlk::launch<uint16_t, 16>(p, stream);
         case 32: return dlk::launch<uint16_t, 32>(p, stream);
         case 64: return dlk::launch<uint16_t, 64>(p, stream);
         case 128: return dlk::launch<uint16_t, 128>(p, stream);
@@ -263,6 +264,7 @@ extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stre
         }
     }
     switch (p.hd) {
+    case 16: return dlk::launch<float, 16>(p, stream);
     case 32: return dlk::launch<float, 32>(p, stream);
     case 64: return dlk::launch<float, 64>(p, stream);
     case 128: return dlk::launch<float, 128>(p, stream);

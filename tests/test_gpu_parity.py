@@ -5,7 +5,6 @@ Tolerances:
   bf16 configs  logits max-abs <= 2e-2 (bf16 weights and KV, f32 accumulation);
   sampling      ids bit-identical given identical logits and key.
 """
-import ctypes as C
 import sys
 
 import numpy as np
@@ -110,13 +109,17 @@ def test_sampler_is_bit_exact_against_the_oracle():
     logits[3] = np.round(logits[3])     # many ties under noise
     t = ct.Tensor.from_numpy(logits, ct.F32, GPU)
     for temperature, key in ((0.0, (0, 0)), (1.0, (11, 12)), (0.7, (2**63 + 5, 3)), (1e-3, (9, 9))):
-        out = ct.Tensor(ct._new(ct.lib().dl_sample, t.handle, temperature, ct.RandomKey(*key))).numpy()
+        out = ct.sample(t, temperature, key).numpy()
         assert np.array_equal(out, oracle.sample(logits, temperature, key)), (temperature, key)
-    greedy = ct.Tensor(ct._new(ct.lib().dl_argmax, t.handle, 1, 0)).numpy()
+    greedy = ct.argmax(t, 1).numpy()
     assert np.array_equal(greedy, [oracle.argmax_row(r) for r in logits])
 
 
 # ------------------------------------------------------------------------------------------ operators
+def G(array, dtype=None):
+    return ct.Tensor.from_numpy(array, dtype, GPU)
+
+
 def test_operators_match_the_oracle():
     say("case: dl_linear / dl_rms_norm / dl_embedding / dl_rotary_embedding / dl_grouped_query_attention")
     rng = np.random.default_rng(5)
@@ -124,42 +127,31 @@ def test_operators_match_the_oracle():
     w = (rng.standard_normal((300, 2048)) * 0.02).astype(np.float32)
     wb = oracle.bf16_encode(w)
     for weight, dtype in ((w, ct.F32), (wb, ct.BF16)):
-        y = ct.Tensor(ct._new(ct.lib().dl_linear, ct.Tensor.from_numpy(x, ct.F32, GPU).handle,
-                              ct.Tensor.from_numpy(weight, dtype, GPU).handle, None)).numpy()
+        y = ct.linear(G(x), G(weight, dtype)).numpy()
         assert rel_err(y, oracle.linear(x, weight)) <= 1e-5
     # K not a multiple of the vector chunk takes the generic kernel
     xs = rng.standard_normal((3, 13)).astype(np.float32)
     ws = rng.standard_normal((7, 13)).astype(np.float32)
-    y = ct.Tensor(ct._new(ct.lib().dl_linear, ct.Tensor.from_numpy(xs, ct.F32, GPU).handle,
-                          ct.Tensor.from_numpy(ws, ct.F32, GPU).handle, None)).numpy()
-    assert rel_err(y, oracle.linear(xs, ws)) <= 1e-5
+    assert rel_err(ct.linear(G(xs), G(ws)).numpy(), oracle.linear(xs, ws)) <= 1e-5
     g = rng.standard_normal(2048).astype(np.float32)
-    eps = C.c_double(1e-5)
-    y = ct.Tensor(ct._new(ct.lib().dl_rms_norm, ct.Tensor.from_numpy(x, ct.F32, GPU).handle, ct._shape([2048]),
-                          ct.Tensor.from_numpy(g, ct.F32, GPU).handle, C.byref(eps))).numpy()
+    y = ct.rms_norm(G(x), [2048], G(g), 1e-5).numpy()
     assert rel_err(y, oracle.rms_norm(x, g, 1e-5)) <= 1e-5
     table = oracle.bf16_encode(rng.standard_normal((50, 64)).astype(np.float32))
     ids = np.array([[3, 49, 0], [7, 7, 12]], np.int64)
-    e = ct.Tensor(ct._new(ct.lib().dl_embedding, ct.Tensor.from_numpy(ids, ct.I64, GPU).handle,
-                          ct.Tensor.from_numpy(table, ct.BF16, GPU).handle))
+    e = ct.embedding(G(ids), G(table, ct.BF16))
     assert e.dtype == ct.BF16 and np.array_equal(e.numpy(), table[ids])
-    bad = ct.Tensor.from_numpy(np.array([50], np.int64), ct.I64, GPU)
-    out = C.c_void_p()
-    assert ct.lib().dl_embedding(bad.handle, ct.Tensor.from_numpy(table, ct.BF16, GPU).handle, C.byref(out)) == 1
-    assert "out of range" in ct.last_error()
+    with pytest.raises(ct.DLError, match="out of range"):
+        ct.embedding(G(np.array([50], np.int64)), G(table, ct.BF16))
     c, s = oracle.rope_tables(64, 9)
     q = rng.standard_normal((2, 3, 9, 64)).astype(np.float32)
-    y = ct.Tensor(ct._new(ct.lib().dl_rotary_embedding, ct.Tensor.from_numpy(q, ct.F32, GPU).handle,
-                          ct.Tensor.from_numpy(c, ct.F32, GPU).handle, ct.Tensor.from_numpy(s, ct.F32, GPU).handle))
+    y = ct.rotary_embedding(G(q), G(c), G(s)).numpy()
     want = oracle.rope(q.transpose(0, 2, 1, 3).reshape(18, 3, 64), c, s, np.repeat(np.arange(9)[None], 2, 0).reshape(-1))
-    assert np.max(np.abs(y.numpy() - want.reshape(2, 9, 3, 64).transpose(0, 2, 1, 3))) <= 1e-6
+    assert np.max(np.abs(y - want.reshape(2, 9, 3, 64).transpose(0, 2, 1, 3))) <= 1e-6
     for L, S in ((1, 200), (3, 70)):
         qq = rng.standard_normal((2, 8, L, 64)).astype(np.float32)
         kk = rng.standard_normal((2, 2, S, 64)).astype(np.float32)
         vv = rng.standard_normal((2, 2, S, 64)).astype(np.float32)
-        y = ct.Tensor(ct._new(ct.lib().dl_grouped_query_attention, ct.Tensor.from_numpy(qq, ct.F32, GPU).handle,
-                              ct.Tensor.from_numpy(kk, ct.F32, GPU).handle, ct.Tensor.from_numpy(vv, ct.F32, GPU).handle,
-                              None)).numpy()
+        y = ct.grouped_query_attention(G(qq), G(kk), G(vv)).numpy()
         assert np.max(np.abs(y - oracle.attention(qq, kk, vv, -1))) <= 1e-5
 
 
