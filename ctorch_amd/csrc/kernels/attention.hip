@@ -17,6 +17,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kRowsMax = 16;
+constexpr int kDecodeChunk = kWaves * kWave; // keys per work-group of the decode kernel
+static_assert(kDecodeChunk == DLK_DECODE_CHUNK, "decode chunk");
+constexpr int kBufferFlags = 0x00020000; // buffer descriptor word 3 for raw (untyped) buffer access on gfx9
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename KT> struct KvTraits;
@@ -167,6 +170,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const dlk_attention
     }
 
     // write results
+    const bool merge_here = p.splits > 1 && p.merge_counters;
 #pragma unroll
     for (int j = 0; j < RPW; ++j) {
         const int r = wave + j * kWaves;
@@ -194,6 +198,53 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const dlk_attention
             }
         }
     }
+    if (!merge_here) return;
+
+    // last-arriver merge: publish this split's partials, count arrivals; the work-group that completes the
+    // count merges all splits of its rows (fixed split order, so the result is deterministic) and resets the
+    // counter for the next launch.  Nothing waits on another work-group.
+    __shared__ int last;
+    __threadfence();
+    __syncthreads();
+    int* counter = p.merge_counters + (static_cast<int64_t>(blockIdx.z) * gridDim.y + blockIdx.y);
+    if (t == 0) last = atomicAdd(counter, 1) == p.splits - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+        const int r = wave + j * kWaves;
+        if (r >= rows) break;
+        const int l = row_l(r), h = row_h(r);
+        const int64_t prow = (static_cast<int64_t>(b) * p.H + h) * p.L + l;
+        const float* ml = p.partial_ml + prow * p.splits * 2;
+        float maximum = -INFINITY;
+        for (int s = 0; s < p.splits; ++s) maximum = fmaxf(maximum, ml[2 * s]);
+        float total = 0.0f, acc[DCOLS];
+#pragma unroll
+        for (int c = 0; c < DCOLS; ++c) acc[c] = 0.0f;
+        for (int s = 0; s < p.splits; ++s) {
+            const float ms = ml[2 * s], ls = ml[2 * s + 1];
+            if (ls <= 0.0f || ms == -INFINITY) continue;
+            const float w = expf(ms - maximum);
+            total += w * ls;
+            const float* o = p.partial_o + (prow * p.splits + s) * HD;
+#pragma unroll
+            for (int c = 0; c < DCOLS; ++c) {
+                const int d = lane + c * kWave;
+                if (d < HD) acc[c] += w * o[d];
+            }
+        }
+        // o * (1/l): the rounding of the single-split path, so a launch whose extra splits are empty matches it
+        const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+        const int64_t m = static_cast<int64_t>(b) * p.L + l;
+#pragma unroll
+        for (int c = 0; c < DCOLS; ++c) {
+            const int d = lane + c * kWave;
+            if (d < HD) p.out[m * p.ldo + static_cast<int64_t>(h) * HD + d] = acc[c] * inv;
+        }
+    }
+    if (t == 0) *counter = 0;
 }
 
 // One wave per (b, h, l) row: merges the split partials with the usual max-rescaled weights.
@@ -230,6 +281,296 @@ __global__ __launch_bounds__(kWave) void attention_combine(const dlk_attention_p
     }
 }
 
+// ------------------------------------------------------------------------------------------ decode
+// One new position per sequence (L = 1) over bf16 K/V, G = H/KV query heads per KV head.  A work-group takes
+// one (sequence, KV head, key chunk of <= 256 keys); each wave one 64-key tile of the chunk, loaded straight
+// into registers when the kernel starts (no dependency precedes them): the K rows with one lane per key for
+// the scores, the V rows with one lane per pair of head-dim columns for P*V.  The scaled q rows are broadcast
+// from LDS.  Each wave normalises its tile on its own (max, exp, sum); the four waves merge through LDS.  Only
+// chunks that hold keys take part: with one such chunk the work-group writes the output itself, otherwise the
+// last of them to finish merges the partials of all (fixed order) and resets its counter.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_decode(
+    const dlk_attention_params p) {
+    constexpr int KCH = HD * 2 / 16;  // 16-byte chunks of a K row
+    constexpr int DL = HD / 2;        // lanes per V row (two bf16 columns per lane)
+    constexpr int KP = kWave / DL;    // keys per V load instruction
+    constexpr int VL = kWave / KP;    // V loads per lane for a 64-key tile
+    constexpr int QN = (G * HD + kThreads - 1) / kThreads;
+    static_assert(DL <= kWave && kWave % DL == 0, "a V row must fit one wave");
+    __shared__ float q_s[G][HD];
+    __shared__ float p_s[kWaves][kWave][G];
+    __shared__ float m_s[kWaves][G], l_s[kWaves][G];
+    __shared__ float o_s[kWaves][G][HD];
+    __shared__ int last;
+
+    const int t = threadIdx.x, lane = t % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int split = blockIdx.x;
+    const int bk = blockIdx.y; // b * KV + kv head
+    const int b = bk / p.KV, kvh = bk % p.KV;
+    const int64_t first = p.position ? *p.position : p.first_host;
+    const int64_t S = first + 1;
+    const int active = static_cast<int>((S + p.chunk - 1) / p.chunk);
+    const bool gather = p.splits > 1 && !p.merge_counters; // the combine pass (or the caller) reads every slot
+    const bool direct = p.splits == 1 || (active == 1 && !gather);
+
+    if (split >= active) {
+        // no keys here: the combine pass still reads this slot
+        if (gather && t < G) {
+            const int64_t slot = (static_cast<int64_t>(b) * p.H + kvh * G + t) * p.splits + split;
+            p.partial_ml[slot * 2] = -INFINITY;
+            p.partial_ml[slot * 2 + 1] = 0.0f;
+        }
+        return;
+    }
+    const int64_t k_begin = static_cast<int64_t>(split) * p.chunk;
+    const int64_t k_end = min(S, k_begin + p.chunk);
+    const int64_t key0 = k_begin + static_cast<int64_t>(kWave) * wave;
+    const size_t head = (static_cast<size_t>(b) * p.KV + kvh) * p.capacity;
+    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + head * HD;
+    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + head * HD;
+
+    // q first, then K and V (vector loads complete in issue order: the q wait never covers K/V).  Keys past
+    // the chunk end are clamped to its last key; their scores are masked.
+    float qv[QN];
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+        const int idx = min(t + i * kThreads, G * HD - 1);
+        qv[i] = p.q[static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G) * HD + idx];
+    }
+    // buffer loads over this wave's tile: offsets are immediates or scalars, and rows past the chunk end read
+    // as zero (their scores are masked below)
+    u32x4 kr[KCH];
+    uint32_t vr[VL];
+    {
+        const int bytes = static_cast<int>(max<int64_t>(0, k_end - key0)) * HD * 2;
+        const __amdgpu_buffer_rsrc_t kres =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase + key0 * HD), 0, bytes, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t vres =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase + key0 * HD), 0, bytes, kBufferFlags);
+        const int krow = lane * HD * 2;
+#pragma unroll
+        for (int c = 0; c < KCH; ++c) kr[c] = __builtin_amdgcn_raw_buffer_load_b128(kres, krow + c * 16, 0, 0);
+        __builtin_amdgcn_sched_barrier(0); // K is issued (and so completes) before V: the scores wait for K only
+        const int vlane = (lane / DL) * HD * 2 + (lane % DL) * 4;
+#pragma unroll
+        for (int j = 0; j < VL; ++j) vr[j] = __builtin_amdgcn_raw_buffer_load_b32(vres, vlane, j * KP * HD * 2, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+        const int idx = t + i * kThreads;
+        if (idx < G * HD) (&q_s[0][0])[idx] = qv[i] * p.scale;
+    }
+    lds_barrier();
+
+    // scores: lane = key.  The q values of chunk c + 1 are read from LDS (broadcast) while chunk c is used: a
+    // batch of 2G reads in flight instead of one read at a time.
+    const bool valid = key0 + lane < k_end;
+    float sc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) sc[g] = 0.0f;
+    float4 qc[G][2], qn[G][2];
+    auto read_q = [&](int c, float4 (&dst)[G][2]) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            dst[g][0] = *reinterpret_cast<const float4*>(&q_s[g][c * 8]);
+            dst[g][1] = *reinterpret_cast<const float4*>(&q_s[g][c * 8 + 4]);
+        }
+    };
+    read_q(0, qc);
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+        if (c + 1 < KCH) read_q(c + 1, qn);
+        __builtin_amdgcn_sched_barrier(0);
+        const float kf[8] = {bf16_lo(kr[c].x), bf16_hi(kr[c].x), bf16_lo(kr[c].y), bf16_hi(kr[c].y),
+                             bf16_lo(kr[c].z), bf16_hi(kr[c].z), bf16_lo(kr[c].w), bf16_hi(kr[c].w)};
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float4 qa = qc[g][0], qb = qc[g][1];
+            sc[g] += qa.x * kf[0] + qa.y * kf[1] + qa.z * kf[2] + qa.w * kf[3] + qb.x * kf[4] + qb.y * kf[5] +
+                     qb.z * kf[6] + qb.w * kf[7];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            qc[g][0] = qn[g][0];
+            qc[g][1] = qn[g][1];
+        }
+    }
+    // the wave's softmax over its tile
+    float m_w[G], l_w[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m_w[g] = wave_max(valid ? sc[g] : -INFINITY);
+        const float pr = valid ? expf(sc[g] - m_w[g]) : 0.0f;
+        l_w[g] = wave_sum(pr);
+        p_s[wave][lane][g] = pr;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+
+    // P*V: lane = (column pair lane % DL, key class lane / DL); the P values of the next PB keys are read from
+    // LDS while the current ones are used
+    constexpr int PB = 8;
+    static_assert(VL % PB == 0, "P batches");
+    float o[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = 0.0f;
+    float pc[PB][G], pn[PB][G];
+    auto read_p = [&](int j0, float (&dst)[PB][G]) {
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            const int kl = (j0 + i) * KP + lane / DL;
+            if constexpr (G % 4 == 0) {
+#pragma unroll
+                for (int g = 0; g < G; g += 4) {
+                    const float4 v4 = *reinterpret_cast<const float4*>(&p_s[wave][kl][g]);
+                    dst[i][g] = v4.x;
+                    dst[i][g + 1] = v4.y;
+                    dst[i][g + 2] = v4.z;
+                    dst[i][g + 3] = v4.w;
+                }
+            } else {
+#pragma unroll
+                for (int g = 0; g < G; ++g) dst[i][g] = p_s[wave][kl][g];
+            }
+        }
+    };
+    read_p(0, pc);
+#pragma unroll
+    for (int j0 = 0; j0 < VL; j0 += PB) {
+        if (j0 + PB < VL) read_p(j0 + PB, pn);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            const float lo = bf16_lo(vr[j0 + i]), hi = bf16_hi(vr[j0 + i]);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                o[g][0] += pc[i][g] * lo;
+                o[g][1] += pc[i][g] * hi;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < PB; ++i)
+#pragma unroll
+            for (int g = 0; g < G; ++g) pc[i][g] = pn[i][g];
+    }
+#pragma unroll
+    for (int off = DL; off < kWave; off <<= 1)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            o[g][0] += __shfl_xor(o[g][0], off, kWave);
+            o[g][1] += __shfl_xor(o[g][1], off, kWave);
+        }
+
+    // merge the four waves
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            m_s[wave][g] = m_w[g];
+            l_s[wave][g] = l_w[g];
+        }
+    }
+    if (lane < DL) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            o_s[wave][g][2 * lane] = o[g][0];
+            o_s[wave][g][2 * lane + 1] = o[g][1];
+        }
+    }
+    lds_barrier();
+    for (int idx = t; idx < G * HD; idx += kThreads) {
+        const int g = idx / HD, d = idx % HD, h = kvh * G + g;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m_s[w][g]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            if (m_s[w][g] == -INFINITY) continue;
+            const float wt = expf(m_s[w][g] - M);
+            L += wt * l_s[w][g];
+            O += wt * o_s[w][g][d];
+        }
+        if (direct) {
+            p.out[static_cast<int64_t>(b) * p.ldo + static_cast<int64_t>(h) * HD + d] = O * (1.0f / L);
+        } else {
+            const int64_t slot = (static_cast<int64_t>(b) * p.H + h) * p.splits + split;
+            p.partial_o[slot * HD + d] = O;
+            if (d == 0) {
+                p.partial_ml[slot * 2] = M;
+                p.partial_ml[slot * 2 + 1] = L;
+            }
+        }
+    }
+    if (direct || gather) return;
+
+    // last-arriver merge over the chunks that hold keys
+    __threadfence();
+    __syncthreads();
+    int* counter = p.merge_counters + bk;
+    if (t == 0) last = atomicAdd(counter, 1) == active - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    for (int idx = t; idx < G * HD; idx += kThreads) {
+        const int g = idx / HD, d = idx % HD, h = kvh * G + g;
+        const int64_t prow = static_cast<int64_t>(b) * p.H + h;
+        const float* ml = p.partial_ml + prow * p.splits * 2;
+        float M = -INFINITY;
+        for (int s = 0; s < active; ++s) M = fmaxf(M, ml[2 * s]);
+        float total = 0.0f, acc = 0.0f;
+        for (int s = 0; s < active; ++s) {
+            const float ms = ml[2 * s], ls = ml[2 * s + 1];
+            if (ls <= 0.0f || ms == -INFINITY) continue;
+            const float w = expf(ms - M);
+            total += w * ls;
+            acc += w * p.partial_o[(prow * p.splits + s) * HD + d];
+        }
+        p.out[static_cast<int64_t>(b) * p.ldo + static_cast<int64_t>(h) * HD + d] = acc * (1.0f / total);
+    }
+    if (t == 0) *counter = 0;
+}
+
+template <int HD>
+int launch_decode(const dlk_attention_params& p, hipStream_t stream) {
+    const dim3 grid(p.splits, p.B * p.KV);
+    switch (p.H / p.KV) {
+    case 1: hipLaunchKernelGGL((attention_decode<HD, 1>), grid, dim3(kThreads), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((attention_decode<HD, 2>), grid, dim3(kThreads), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((attention_decode<HD, 4>), grid, dim3(kThreads), 0, stream, p); break;
+    case 8:
+        if constexpr (HD == 64) {
+            hipLaunchKernelGGL((attention_decode<HD, 8>), grid, dim3(kThreads), 0, stream, p);
+            break;
+        }
+        return static_cast<int>(hipErrorInvalidValue);
+    default: return static_cast<int>(hipErrorInvalidValue);
+    }
+    int status = static_cast<int>(hipGetLastError());
+    if (status != 0 || p.splits == 1 || p.partials_only || p.merge_counters) return status;
+    const int64_t combine_rows = static_cast<int64_t>(p.B) * p.H;
+    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kWave), 0, stream, p);
+    return static_cast<int>(hipGetLastError());
+}
+
+/// The decode kernel serves one new position over bf16 K/V with HD 64 (G in {1, 2, 4, 8}) or 128 (G <= 4) and
+/// chunks of at most four 64-key tiles.
+bool decode_path(const dlk_attention_params& p) {
+    const int G = p.H / p.KV;
+    return p.kv_bf16 && p.L == 1 && (p.hd == 64 || p.hd == 128) && (G == 1 || G == 2 || G == 4 || (G == 8 && p.hd == 64)) &&
+           p.chunk <= kDecodeChunk && p.chunk % kWave == 0;
+}
+
 template <typename KT, int HD>
 int launch(const dlk_attention_params& p, hipStream_t stream) {
     // 64-key tiles; f32 K/V with 128-wide heads use 32-key tiles to keep the LDS footprint under 64 KB
@@ -239,7 +580,7 @@ int launch(const dlk_attention_params& p, hipStream_t stream) {
     dim3 grid(p.splits, row_blocks, p.B * p.KV);
     hipLaunchKernelGGL((attention_kernel<KT, HD, T>), grid, dim3(kThreads), 0, stream, p);
     int status = static_cast<int>(hipGetLastError());
-    if (status != 0 || p.splits == 1) return status;
+    if (status != 0 || p.splits == 1 || p.partials_only || p.merge_counters) return status;
     const int64_t combine_rows = static_cast<int64_t>(p.B) * p.H * p.L;
     hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kWave), 0, stream, p);
     return static_cast<int>(hipGetLastError());
@@ -248,12 +589,17 @@ int launch(const dlk_attention_params& p, hipStream_t stream) {
 } // namespace
 } // namespace dlk
 
+extern "C" int dlk_attention_row_blocks(int heads, int kv_heads, int length) {
+    return (heads / kv_heads * length + dlk::kRowsMax - 1) / dlk::kRowsMax;
+}
+
 extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stream_handle) {
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
     const dlk_attention_params& p = *params;
     if (p.B <= 0 || p.L <= 0 || p.KV <= 0 || p.H % p.KV != 0 || p.splits <= 0 || p.chunk <= 0 ||
         (p.splits > 1 && (!p.partial_o || !p.partial_ml)) || (p.splits > 1 && p.chunk % 64 != 0))
         return static_cast<int>(hipErrorInvalidValue);
+    if (dlk::decode_path(p)) return p.hd == 64 ? dlk::launch_decode<64>(p, stream) : dlk::launch_decode<128>(p, stream);
     if (p.kv_bf16) {
         switch (p.hd) {
         case 16: return dlk::launch<uint16_t, 16>(p, stream);

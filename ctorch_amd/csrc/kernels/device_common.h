@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "kernels/kernels.h"
 
 namespace dlk {
@@ -116,15 +118,34 @@ __device__ __forceinline__ bool prefer(double a, int64_t ia, double b, int64_t i
     return ia < ib;
 }
 
+// Wave64 all-reductions without LDS: DPP steps reduce each row of 16 lanes (pair, quad, half-row, row; every
+// lane ends with its row's value), then the four row values are read into scalars and combined.  The result
+// is wave-uniform and identical in every lane.  All 64 lanes must be active.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+    constexpr int kQuadSwap1 = 0xB1; // quad_perm [1, 0, 3, 2]
+    constexpr int kQuadSwap2 = 0x4E; // quad_perm [2, 3, 0, 1]
+    constexpr int kHalfMirror = 0x141;
+    constexpr int kRowMirror = 0x140;
+    auto dpp = [](float x, auto ctrl) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    v = op(v, dpp(v, std::integral_constant<int, kQuadSwap1>{}));
+    v = op(v, dpp(v, std::integral_constant<int, kQuadSwap2>{}));
+    v = op(v, dpp(v, std::integral_constant<int, kHalfMirror>{}));
+    v = op(v, dpp(v, std::integral_constant<int, kRowMirror>{}));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return op(op(r0, r1), op(r2, r3));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
-    return v;
+    return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
-    return v;
+    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 } // namespace dlk

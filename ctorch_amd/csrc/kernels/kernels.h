@@ -82,7 +82,8 @@ typedef struct dlk_gemv_params {
     int partial_blocks;
 } dlk_gemv_params;
 
-/* Number of work-groups the launch uses for its n range (the LOGITS partial row length). */
+/* Waves of the persistent launch (the LOGITS partial row length: one sampling candidate per wave); -1 when no
+   kernel fits the parameters.  Depends on the current device's CU count and the kernel's occupancy. */
 int dlk_gemv_blocks(const dlk_gemv_params* p);
 int dlk_gemv(const dlk_gemv_params* p, dlh_stream stream);
 
@@ -112,7 +113,16 @@ typedef struct dlk_attention_params {
     int chunk;               /* keys per split (multiple of the tile) */
     float* partial_o;        /* [B*H*L, splits, hd] */
     float* partial_ml;       /* [B*H*L, splits, 2] */
+    int partials_only;       /* splits > 1 without merge_counters: leave the merge to the caller */
+    int* merge_counters;     /* splits > 1: [B*KV*row_blocks] zeroed counters; the last split work-group of
+                              * each (b, kv head, row block) merges the partials and resets its counter */
 } dlk_attention_params;
+
+/* Keys per split that the one-position decode kernel takes (bf16 K/V, L = 1): chunk <= this uses it. */
+#define DLK_DECODE_CHUNK 256
+
+/* Query-row blocks of one (b, kv head) in dlk_attention (merge_counters has B*KV*blocks entries). */
+int dlk_attention_row_blocks(int heads, int kv_heads, int length);
 
 int dlk_attention(const dlk_attention_params* p, dlh_stream stream);
 
@@ -141,10 +151,11 @@ int dlk_sample_partials(const float* logits, int64_t rows, int64_t n, int mode, 
                         dlk_sample_partial* partial, int blocks, dlh_stream stream);
 int dlk_sample_blocks(int64_t n);
 /* Reduces partial [rows, blocks] to ids: out[r] (may be NULL), next_ids[r] (may be NULL), and
- * tokens[r * token_stride + *step] when tokens != NULL; then advances *step by one if step != NULL. */
+ * tokens[r * token_stride + *step] when tokens != NULL; then advances *step by one if step != NULL.
+ * With embedding != NULL it also writes the next step's input rows x[r, :] = f32(embedding[id, :]). */
 int dlk_sample_finalize(const dlk_sample_partial* partial, int64_t rows, int blocks, int64_t* out,
                         int64_t* next_ids, int64_t* tokens, int64_t token_stride, int64_t* step,
-                        dlh_stream stream);
+                        const void* embedding, int embedding_dtype, int64_t width, float* x, dlh_stream stream);
 /* Keyed Philox: mode 0 uniform [low, high), mode 1 standard normal times scale; output f32 or bf16. */
 int dlk_random(uint64_t seed, uint64_t stream_bits, int64_t count, int mode, double low, double high,
                double scale, void* out, int out_dtype, dlh_stream stream);

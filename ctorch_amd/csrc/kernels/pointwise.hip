@@ -168,45 +168,52 @@ __global__ __launch_bounds__(kThreads) void sample_partials_kernel(const float* 
     }
 }
 
-// One work-group reduces every row's candidates in parallel lanes (the preference is associative and
-// commutative on distinct indices, so the reduction order does not change the result).
-__global__ __launch_bounds__(kThreads) void sample_finalize_kernel(const dlk_sample_partial* partial, int64_t rows,
-                                                                   int blocks, int64_t* out, int64_t* next_ids,
-                                                                   int64_t* tokens, int64_t token_stride,
-                                                                   int64_t* step) {
-    __shared__ double best_score[kThreads];
-    __shared__ int64_t best_index[kThreads];
+// One work-group of 1024 threads reduces every row's candidates (the preference is associative and
+// commutative on distinct indices, so the reduction order does not change the result), then gathers the
+// chosen token's embedding row as the next step's input.
+constexpr int kFinalizeThreads = 1024;
+__global__ __launch_bounds__(kFinalizeThreads) void sample_finalize_kernel(
+    const dlk_sample_partial* partial, int64_t rows, int blocks, int64_t* out, int64_t* next_ids, int64_t* tokens,
+    int64_t token_stride, int64_t* step, const void* embedding, int embedding_dtype, int64_t width, float* x) {
+    __shared__ double wave_score[kFinalizeThreads / kWave];
+    __shared__ int64_t wave_index[kFinalizeThreads / kWave];
+    __shared__ int64_t chosen;
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const int64_t column = step ? *step : 0;
     for (int64_t row = 0; row < rows; ++row) {
         double best = 0.0;
         int64_t index = -1;
-        for (int i = threadIdx.x; i < blocks; i += kThreads) {
+        for (int i = threadIdx.x; i < blocks; i += kFinalizeThreads) {
             const dlk_sample_partial c = partial[row * blocks + i];
             if (c.index < 0) continue;
             if (index < 0 || prefer(c.score, c.index, best, index)) { best = c.score; index = c.index; }
         }
-        best_score[threadIdx.x] = best;
-        best_index[threadIdx.x] = index;
-        __syncthreads();
-        for (int width = kThreads / 2; width > 0; width >>= 1) {
-            if (threadIdx.x < width) {
-                const int64_t j = best_index[threadIdx.x + width];
-                if (j >= 0) {
-                    const double s = best_score[threadIdx.x + width];
-                    const int64_t i = best_index[threadIdx.x];
-                    if (i < 0 || prefer(s, j, best_score[threadIdx.x], i)) {
-                        best_score[threadIdx.x] = s;
-                        best_index[threadIdx.x] = j;
-                    }
-                }
-            }
-            __syncthreads();
+        for (int offset = kWave / 2; offset > 0; offset >>= 1) {
+            const double s = __shfl_xor(best, offset, kWave);
+            const int64_t j = __shfl_xor(index, offset, kWave);
+            if (j >= 0 && (index < 0 || prefer(s, j, best, index))) { best = s; index = j; }
         }
+        if (lane == 0) { wave_score[wave] = best; wave_index[wave] = index; }
+        __syncthreads();
         if (threadIdx.x == 0) {
-            const int64_t token = best_index[0];
-            if (out) out[row] = token;
-            if (next_ids) next_ids[row] = token;
-            if (tokens) tokens[row * token_stride + column] = token;
+            double b = 0.0;
+            int64_t bi = -1;
+            for (int w = 0; w < kFinalizeThreads / kWave; ++w) {
+                const int64_t j = wave_index[w];
+                if (j >= 0 && (bi < 0 || prefer(wave_score[w], j, b, bi))) { b = wave_score[w]; bi = j; }
+            }
+            chosen = bi;
+            if (out) out[row] = bi;
+            if (next_ids) next_ids[row] = bi;
+            if (tokens) tokens[row * token_stride + column] = bi;
+        }
+        __syncthreads();
+        if (embedding && x) {
+            const int64_t id = chosen < 0 ? 0 : chosen;
+            for (int64_t i = threadIdx.x; i < width; i += kFinalizeThreads)
+                x[row * width + i] = embedding_dtype == DLK_BF16
+                                         ? bf16_to_f32(static_cast<const uint16_t*>(embedding)[id * width + i])
+                                         : static_cast<const float*>(embedding)[id * width + i];
         }
         __syncthreads();
     }
@@ -373,9 +380,11 @@ int dlk_sample_partials(const float* logits, int64_t rows, int64_t n, int mode, 
 }
 
 int dlk_sample_finalize(const dlk_sample_partial* partial, int64_t rows, int blocks, int64_t* out, int64_t* next_ids,
-                        int64_t* tokens, int64_t token_stride, int64_t* step, dlh_stream stream) {
-    hipLaunchKernelGGL(dlk::sample_finalize_kernel, dim3(1), dim3(kThreads), 0, as_stream(stream), partial, rows,
-                       blocks, out, next_ids, tokens, token_stride, step);
+                        int64_t* tokens, int64_t token_stride, int64_t* step, const void* embedding,
+                        int embedding_dtype, int64_t width, float* x, dlh_stream stream) {
+    hipLaunchKernelGGL(dlk::sample_finalize_kernel, dim3(1), dim3(dlk::kFinalizeThreads), 0, as_stream(stream),
+                       partial, rows, blocks, out, next_ids, tokens, token_stride, step, embedding, embedding_dtype,
+                       width, x);
     return dlk::status();
 }
 

@@ -11,7 +11,9 @@ namespace dl::detail {
 /// Scratch of one decode chunk of `rows` = B * L activation rows.
 struct DecodeWorkspace {
     Index rows = 0, splits_capacity = 0;
-    Tensor q, attention, hidden, activation, partial_o, partial_ml, lora_query, lora_value;
+    Tensor q, attention, hidden, activation, partial_o, partial_ml, lora_query, lora_value, counters;
+    /// Zeroed i32 split-merge counters for the attention kernel (at least `count`).
+    int* merge_counters(Index count, Device device, GpuContext& context);
     void ensure(const nn::TransformerDecoderLayer& layer, Index rows, Index heads_total, Index hidden_features,
                 int splits, Device device);
 };

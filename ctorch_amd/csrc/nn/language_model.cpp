@@ -64,11 +64,13 @@ void DecoderLM::forward_chunk(const Index* ids, Index batch, Index length, std::
     auto observe = [&](const char* name, double bytes) { if (observer) observer->before(name, bytes); };
     auto done = [&]() { if (observer) observer->after(); };
 
-    observe("embedding", static_cast<double>(rows * d) * static_cast<double>(element_size(embedding_->weight().dtype())));
-    hip_check(dlk_embedding(ids, rows, embedding_->weight().data<void>(), dlk_dtype(embedding_->weight().dtype()),
-                            embedding_->weight().size(0), d, x, DLK_F32, context_->error_flag, context_->stream),
-              "embedding");
-    done();
+    if (ids) {
+        observe("embedding", static_cast<double>(rows * d) * static_cast<double>(element_size(embedding_->weight().dtype())));
+        hip_check(dlk_embedding(ids, rows, embedding_->weight().data<void>(), dlk_dtype(embedding_->weight().dtype()),
+                                embedding_->weight().size(0), d, x, DLK_F32, context_->error_flag, context_->stream),
+                  "embedding");
+        done();
+    }
 
     const auto& first = decoder_->layer(0).attention();
     int splits = 1, chunk = 64;
@@ -105,6 +107,7 @@ void DecoderLM::forward_chunk(const Index* ids, Index batch, Index length, std::
     if (sample_mode > 0) {
         p.key_label = static_cast<const Index*>(step_.data<void>());
         const int blocks = dlk_gemv_blocks(&p);
+        if (blocks <= 0) throw std::invalid_argument("LM head: no projection kernel fits this shape");
         if (!partial_.defined() || blocks_ != blocks || partial_.numel() < batch * blocks * 2) {
             partial_ = empty_tensor({batch * blocks * 2}, DType::i64, device);
             blocks_ = blocks;
@@ -117,10 +120,13 @@ void DecoderLM::forward_chunk(const Index* ids, Index batch, Index length, std::
     done();
     if (sample_mode > 0) {
         observe("sample_finalize", 0.0);
+        // the sampled ids are fed back: their embedding rows become the next step's input x[0:B]
         hip_check(dlk_sample_finalize(static_cast<const dlk_sample_partial*>(partial_.data<void>()), batch, blocks_,
                                       nullptr, static_cast<Index*>(mutable_data(next_ids_)),
                                       tokens_.defined() ? static_cast<Index*>(mutable_data(tokens_)) : nullptr,
-                                      token_columns_, static_cast<Index*>(mutable_data(step_)), context_->stream),
+                                      token_columns_, static_cast<Index*>(mutable_data(step_)),
+                                      embedding_->weight().data<void>(), dlk_dtype(embedding_->weight().dtype()), d, x,
+                                      context_->stream),
                   "sample");
         done();
     }
@@ -180,7 +186,7 @@ DecoderLM::RunResult DecoderLM::run(const Tensor& prompt, std::span<nn::KVCache>
         const Index eager_steps = use_graph ? std::min<Index>(steps, 2) : steps;
         for (Index s = 1; s < eager_steps; ++s) {
             mark_start(s);
-            forward_chunk(next_ids_.data<Index>(), B, 1, cache, mode, temperature, key, use_graph, nullptr);
+            forward_chunk(nullptr, B, 1, cache, mode, temperature, key, use_graph, nullptr);
         }
         if (use_graph && steps > 2) {
             // capture one single-token step; host lengths are restored because capture does not execute
@@ -189,7 +195,7 @@ DecoderLM::RunResult DecoderLM::run(const Tensor& prompt, std::span<nn::KVCache>
             release_graph();
             hip_check(dlh_capture_begin(context_->stream), "graph capture");
             try {
-                forward_chunk(next_ids_.data<Index>(), B, 1, cache, mode, temperature, key, true, nullptr);
+                forward_chunk(nullptr, B, 1, cache, mode, temperature, key, true, nullptr);
             } catch (...) {
                 dlh_graph discard = nullptr;
                 (void)dlh_capture_end(context_->stream, &discard);
@@ -284,7 +290,7 @@ std::vector<KernelTiming> DecoderLM::profile(const Tensor& ids, std::span<nn::KV
     tokens_ = Tensor();
     EventObserver observer(context_->stream);
     for (Index s = 0; s < steps; ++s)
-        forward_chunk(next_ids_.data<Index>(), B, 1, cache, 1, 0.0, {0, 0}, false, &observer);
+        forward_chunk(s == 0 ? next_ids_.data<Index>() : nullptr, B, 1, cache, 1, 0.0, {0, 0}, false, &observer);
     hip_check(dlh_stream_synchronize(context_->stream), "profile");
     std::vector<KernelTiming> out;
     for (const auto& p : observer.pending) {

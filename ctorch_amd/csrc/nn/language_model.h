@@ -36,8 +36,9 @@ public:
 private:
     struct StepBuffers;
     void check_caches(std::span<nn::KVCache> cache, Index batch, Index length) const;
-    /// Feeds B*L ids already on the device; writes logits of the last position and, when sample_mode > 0,
-    /// samples into the token / next-id buffers (key label = device step counter).
+    /// Feeds B*L ids already on the device (ids == nullptr: the input rows were already gathered into x_ by
+    /// the previous step's sampler); writes logits of the last position and, when sample_mode > 0, samples
+    /// into the token / next-id buffers (key label = device step counter) and gathers the next input rows.
     void forward_chunk(const Index* ids, Index batch, Index length, std::span<nn::KVCache> cache, int sample_mode,
                        double temperature, RandomKey key, bool capacity_splits, LaunchObserver* observer);
     void release_graph();

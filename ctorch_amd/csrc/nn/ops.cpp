@@ -80,6 +80,12 @@ void linear_into(const float* x, Index rows, Index k, const Tensor& weight, cons
 
 void attention_split(Index batch, Index kv_heads, Index length, Index source, int& splits, int& chunk) {
     constexpr Index tile = 64;
+    if (length == 1) {
+        // one new position: splits of DLK_DECODE_CHUNK keys, one 64-key tile per wave of a work-group
+        splits = static_cast<int>(std::max<Index>(1, (source + DLK_DECODE_CHUNK - 1) / DLK_DECODE_CHUNK));
+        chunk = DLK_DECODE_CHUNK;
+        return;
+    }
     const Index groups = batch * kv_heads;
     const Index tiles = std::max<Index>(1, (source + tile - 1) / tile);
     Index wanted = 1;
@@ -258,7 +264,7 @@ Tensor sample(const Tensor& logits, double temperature, RandomKey key) {
                                   blocks, context.stream),
               "sample");
     hip_check(dlk_sample_finalize(parts, rows, blocks, static_cast<Index*>(mutable_data(out)), nullptr, nullptr, 0,
-                                  nullptr, context.stream),
+                                  nullptr, nullptr, 0, 0, nullptr, context.stream),
               "sample");
     return out;
 }
