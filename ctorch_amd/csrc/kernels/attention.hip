@@ -19,7 +19,6 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kRowsMax = 16;
 constexpr int kDecodeChunk = kWaves * kWave; // keys per work-group of the decode kernel
 static_assert(kDecodeChunk == DLK_DECODE_CHUNK, "decode chunk");
-constexpr int kBufferFlags = 0x00020000; // buffer descriptor word 3 for raw (untyped) buffer access on gfx9
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename KT> struct KvTraits;

@@ -12,6 +12,8 @@
 namespace dlk {
 
 constexpr int kWave = 64;
+/// Buffer descriptor word 3 for raw (untyped) buffer access on gfx9-family GPUs.
+constexpr int kBufferFlags = 0x00020000;
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }

@@ -2,7 +2,7 @@
 //
 // The grid is persistent: one wave per row group, capped at the number of waves the chosen kernel keeps
 // resident on the device (its occupancy times the CU count), so every wave streams from the start and none
-// waits for another to retire.  LOGITS launches write one sampling candidate per wave.
+// waits for another to retire.  LOGITS launches write one sampling candidate per work-group.
 #include "kernels/gemv_impl.h"
 
 #include <mutex>
@@ -63,9 +63,9 @@ int launch_waves(const dlk_gemv_params& p) {
 } // namespace
 
 extern "C" int dlk_gemv_blocks(const dlk_gemv_params* p) {
-    // LOGITS: one sampling candidate per wave of the launch
+    // LOGITS: one sampling candidate per work-group of the launch
     const int waves = launch_waves(*p);
-    return waves > 0 ? waves : -1;
+    return waves > 0 ? (waves + dlk::gemv::kWavesPerBlock - 1) / dlk::gemv::kWavesPerBlock : -1;
 }
 
 extern "C" int dlk_gemv(const dlk_gemv_params* params, dlh_stream stream_handle) {
@@ -84,9 +84,9 @@ extern "C" int dlk_gemv(const dlk_gemv_params* params, dlh_stream stream_handle)
             if (params->seg_rows[s] % 2 != 0 || params->head_dim % 2 != 0) return static_cast<int>(hipErrorInvalidValue);
     const int waves = launch_waves(*params);
     if (waves <= 0) return static_cast<int>(hipErrorInvalidValue);
-    if (params->epilogue == DLK_EPI_LOGITS && params->sample_mode != 0 && params->partial_blocks != waves)
-        return static_cast<int>(hipErrorInvalidValue);
     const int blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (params->epilogue == DLK_EPI_LOGITS && params->sample_mode != 0 && params->partial_blocks != blocks)
+        return static_cast<int>(hipErrorInvalidValue);
     const int max_rows = plan_of(params->K, params->w_bf16 != 0, params->epilogue).mt_max;
     dlk_gemv_params p = *params;
     // activation rows are processed max_rows at a time (weights re-streamed per chunk of rows)

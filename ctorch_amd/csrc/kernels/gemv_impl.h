@@ -33,6 +33,7 @@ constexpr int kLdsBytes = 60 * 1024;  // staged activation row of the fallback k
 constexpr int kLdsSteps = 4;          // chunks per lane per step in the fallback kernel
 constexpr int kLdsXL = 15;            // float4 activation loads per thread in the fallback (K <= 15360)
 constexpr int kRegBudget = 192;       // VGPRs for activations + two weight buffers in the register kernel
+constexpr int kOutOfRange = 0x7fffff00; // buffer offset past any range: the load returns zeros, touches nothing
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr bool pair_epilogue(int epi) { return epi == DLK_EPI_QKV || epi == DLK_EPI_SWIGLU; }
@@ -185,19 +186,44 @@ template <int R, int CPI> struct Step {
     float aux0, aux1;
 };
 
+// Per activation row of the launch (QKV): its sequence and absolute position, computed once per kernel in
+// scalars (integer division stays out of the per-group path).
+template <int MT> struct Rows {
+    int batch[MT];
+    int64_t pos[MT];
+    __device__ Rows(const dlk_gemv_params& p, bool used) {
+        const int64_t first = used ? *p.position : 0;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const int mg = static_cast<int>(p.m_base) + m;
+            batch[m] = used ? mg / p.length : 0;
+            pos[m] = used ? first + mg % p.length : 0;
+        }
+    }
+    // the position of row m for a lane-dependent m (selects, no indexed access)
+    __device__ __forceinline__ int64_t pos_of(int m) const {
+        int64_t v = pos[0];
+#pragma unroll
+        for (int i = 1; i < MT; ++i)
+            if (m == i) v = pos[i];
+        return v;
+    }
+};
+
 template <int MT, int R, int EPI, typename WT>
-__device__ __forceinline__ void load_aux(const dlk_gemv_params& p, const Group<WT>& grp, int lane, int64_t first,
+__device__ __forceinline__ void load_aux(const dlk_gemv_params& p, const Group<WT>& grp, int lane, const Rows<MT>& rows,
                                          float& aux0, float& aux1) {
     if constexpr (EPI == DLK_EPI_RESIDUAL || EPI == DLK_EPI_QKV) {
         // lanes past the outputs load a clamped, valid address; their values are never used
         const int m = min(min(lane / R, MT - 1), p.M - 1);
-        const int n = min(grp.n0 + lane % R, grp.rows - 1);
         if constexpr (EPI == DLK_EPI_RESIDUAL) {
+            const int n = min(grp.n0 + lane % R, grp.rows - 1);
             aux0 = p.residual[static_cast<int64_t>(m) * p.ldres + n];
         } else {
-            const int64_t pos = first + (p.m_base + m) % p.length;
+            // rows come in even pairs and n0 is even, so the column of n0 + r in its head is (n0 % hd) + r
             const int hd = p.head_dim;
-            const int64_t table = pos * (hd / 2) + (n % hd) / 2;
+            const int d = grp.n0 % hd + lane % R;
+            const int64_t table = rows.pos_of(m) * (hd / 2) + d / 2;
             aux0 = p.cosine[table];
             aux1 = p.sine[table];
         }
@@ -207,7 +233,8 @@ __device__ __forceinline__ void load_aux(const dlk_gemv_params& p, const Group<W
 // The epilogue of one finished group; v[m][r] holds the full dot products (every lane has them).
 template <typename WT, int MT, int R, int EPI, typename Seg>
 __device__ __forceinline__ void finish_group(const dlk_gemv_params& p, const Seg& sg, const float (&v)[MT][R], int g,
-                                             int lane, int64_t first, float aux0, float aux1, Candidates<MT>& cand) {
+                                             int lane, const Rows<MT>& rows, float aux0, float aux1,
+                                             Candidates<MT>& cand) {
     using Traits = WeightTraits<WT>;
     constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
     constexpr int OUTS = SWIGLU ? R / 2 : R;
@@ -265,10 +292,9 @@ __device__ __forceinline__ void finish_group(const dlk_gemv_params& p, const Seg
                     value += dv * p.lora_scale;
                     partner += dp * p.lora_scale;
                 }
-                const int64_t b = mg / p.length, l = mg % p.length;
-                const int64_t pos = first + l;
+                const int64_t b = rows.batch[m], pos = rows.pos[m];
                 const int hd = p.head_dim;
-                const int d = n % hd;
+                const int head = n0 / hd, d = n0 % hd + r;
                 if (seg < 2) {
                     const float c = aux0, s = aux1;
                     // even: x_e c - x_o s ; odd: x_e s + x_o c (interleaved pairs, src/ops/contraction.cpp:44-49)
@@ -277,7 +303,6 @@ __device__ __forceinline__ void finish_group(const dlk_gemv_params& p, const Seg
                 if (seg == 0) {
                     p.y[mg * p.ldy + n] = value;
                 } else {
-                    const int head = n / hd;
                     const int64_t index = ((b * p.kv_heads + head) * p.cache_capacity + pos) * hd + d;
                     void* cache = seg == 1 ? p.k_cache : p.v_cache;
                     if (p.cache_bf16) static_cast<uint16_t*>(cache)[index] = f32_to_bf16(value);
@@ -305,19 +330,37 @@ __device__ __forceinline__ void finish_group(const dlk_gemv_params& p, const Seg
     }
 }
 
+// End of a launch.  LOGITS: the work-group's waves pool their sampling candidates in LDS and wave 0 writes the
+// best one per activation row as the work-group's partial (every wave of the work-group must get here).
 template <int MT, int EPI>
 __device__ __forceinline__ void finish_kernel(const dlk_gemv_params& p, const Candidates<MT>& cand, int lane,
-                                              int my_wave) {
+                                              int wave_in_block) {
     if constexpr (EPI == DLK_EPI_LOGITS) {
-        if (p.sample_mode != 0) {
+        __shared__ double pool_score[kWavesPerBlock][MT];
+        __shared__ int64_t pool_index[kWavesPerBlock][MT];
+        if (p.sample_mode == 0) return;
 #pragma unroll
-            for (int m = 0; m < MT; ++m)
-                if (lane == m && m < p.M && my_wave < p.partial_blocks) {
-                    dlk_sample_partial out;
-                    out.score = cand.score[m];
-                    out.index = cand.index[m];
-                    p.partial[(p.m_base + m) * p.partial_blocks + my_wave] = out;
+        for (int m = 0; m < MT; ++m)
+            if (lane == m) {
+                pool_score[wave_in_block][m] = cand.score[m];
+                pool_index[wave_in_block][m] = cand.index[m];
+            }
+        lds_barrier();
+        if (wave_in_block == 0 && lane < MT && lane < p.M) {
+            double best = 0.0;
+            int64_t index = -1;
+#pragma unroll
+            for (int w = 0; w < kWavesPerBlock; ++w) {
+                const int64_t j = pool_index[w][lane];
+                if (j >= 0 && (index < 0 || prefer(pool_score[w][lane], j, best, index))) {
+                    best = pool_score[w][lane];
+                    index = j;
                 }
+            }
+            dlk_sample_partial out;
+            out.score = best;
+            out.index = index;
+            p.partial[(p.m_base + lane) * p.partial_blocks + blockIdx.x] = out;
         }
     }
     if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL) {
@@ -326,13 +369,10 @@ __device__ __forceinline__ void finish_kernel(const dlk_gemv_params& p, const Ca
     }
 }
 
-// Runs the streaming loop over `count` >= 1 steps with one step in flight beyond the one being used: loads in
-// the loop body are unconditional, the last step is peeled.  load(k, buf) / use(k, buf); prologue() runs while
-// the first step's loads are in flight.
-template <typename Buf, typename Load, typename Use, typename Prologue>
-__device__ __forceinline__ void stream_steps(int count, Buf& a, Buf& b, Load&& load, Use&& use, Prologue&& prologue) {
-    load(0, a);
-    prologue();
+// Runs the streaming loop over `count` >= 1 steps with one step in flight beyond the one being used; step 0 is
+// already loaded into `a` by the caller.  Loads in the loop body are unconditional, the last step is peeled.
+template <typename Buf, typename Load, typename Use>
+__device__ __forceinline__ void stream_steps(int count, Buf& a, Buf& b, Load&& load, Use&& use) {
     int k = 0;
     for (;;) {
         if (k + 1 >= count) {
@@ -353,7 +393,9 @@ __device__ __forceinline__ void stream_steps(int count, Buf& a, Buf& b, Load&& l
 }
 
 // ------------------------------------------------------------------------------------------ register kernel
-// CPI = 16-byte chunks per lane per row: the whole row in one step (K <= 64 * CPI * chunk).
+// CPI = 16-byte chunks per lane per row: the whole row in one step (K <= 64 * CPI * chunk).  Each wave loads
+// its own copy of the activation chunks it needs (lane l: chunks l, l + 64, ...) and applies the RMSNorm
+// in-wave; on MI355X this beat staging the rows once per work-group in LDS at every decode shape.
 template <typename WT, int MT, int R, int CPI, int EPI, bool NORM>
 __global__ __launch_bounds__(kThreads) void gemv_reg(const dlk_gemv_params p) {
     using Traits = WeightTraits<WT>;
@@ -363,14 +405,23 @@ __global__ __launch_bounds__(kThreads) void gemv_reg(const dlk_gemv_params p) {
     const int nch = K / CH;
     const int lane = threadIdx.x % kWave;
     // wave-uniform in a scalar register: group and segment selection stay scalar (no per-lane branches)
-    const int my_wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave);
+    const int wave_in_block = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int my_wave = blockIdx.x * kWavesPerBlock + wave_in_block;
     const int waves = gridDim.x * kWavesPerBlock;
     const Segments<WT, R, SWIGLU> sg(p);
     const int groups = groups_of(p, R, SWIGLU);
-    if (my_wave >= groups) return; // no barrier in this kernel; only the last work-group has idle waves
-    const int my_groups = (groups - my_wave + waves - 1) / waves;
+    // idle waves (only in the last work-group) exit, except in LOGITS, whose end pools the work-group's waves
+    if constexpr (EPI != DLK_EPI_LOGITS) {
+        if (my_wave >= groups) return;
+    }
+    const int my_groups = my_wave < groups ? (groups - my_wave + waves - 1) / waves : 0;
+    const bool norm = NORM && p.apply_norm;
+    const bool affine = norm && p.norm_weight;
 
-    // activations and norm weights first: waiting for them never waits for the weight stream
+    // 1. activations and norm weights first (their wait never covers the weight loads issued after them).  No
+    // load sits in a branch: a load on one path only would make the first wait drain every load.  The norm
+    // weights come through a bounds-checked buffer load (16 bytes at the element offset for either dtype;
+    // bytes past the vector read as zero).
     float x[MT][CPI][CH];
 #pragma unroll
     for (int i = 0; i < CPI; ++i) {
@@ -388,57 +439,53 @@ __global__ __launch_bounds__(kThreads) void gemv_reg(const dlk_gemv_params p) {
             }
         }
     }
-    const bool norm = NORM && p.apply_norm;
-    const bool affine = norm && p.norm_weight;
-    float g[NORM ? CPI : 1][CH];
-    if (affine) {
+    u32x4 graw[NORM ? CPI : 1][CH / 4];
+    if constexpr (NORM) {
+        const int esize = p.norm_bf16 ? 2 : 4;
+        const __amdgpu_buffer_rsrc_t gres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<void*>(affine ? p.norm_weight : static_cast<const void*>(p.x)), 0, affine ? K * esize : 0,
+            kBufferFlags);
 #pragma unroll
         for (int i = 0; i < CPI; ++i) {
             const int c = min(lane + kWave * i, nch - 1);
 #pragma unroll
-            for (int j = 0; j < CH; j += 4) {
-                if (p.norm_bf16) {
-                    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.norm_weight) + c * CH + j);
-                    g[i][j] = bf16_lo(w.x);
-                    g[i][j + 1] = bf16_hi(w.x);
-                    g[i][j + 2] = bf16_lo(w.y);
-                    g[i][j + 3] = bf16_hi(w.y);
-                } else {
-                    const float4 w = *reinterpret_cast<const float4*>(static_cast<const float*>(p.norm_weight) + c * CH + j);
-                    g[i][j] = w.x;
-                    g[i][j + 1] = w.y;
-                    g[i][j + 2] = w.z;
-                    g[i][j + 3] = w.w;
-                }
+            for (int j = 0; j < CH / 4; ++j) {
+                // bf16 weights: the first 16 bytes already hold the chunk; later parts read past the range
+                // (no memory access, zeros) instead of branching around the load
+                const int offset = j > 0 && esize == 2 ? kOutOfRange : (c * CH + 4 * j) * esize;
+                graw[i][j] = __builtin_amdgcn_raw_buffer_load_b128(gres, offset, 0, 0);
             }
         }
     }
 
     Candidates<MT> cand;
     init_candidates<MT, EPI>(p, cand);
-    const int64_t first = EPI == DLK_EPI_QKV ? *p.position : 0;
-
+    const Rows<MT> rows(p, EPI == DLK_EPI_QKV);
     auto load = [&](int k, Step<R, CPI>& buf) {
-        const auto grp = sg.locate(my_wave + k * waves);
+        const auto grp = sg.locate(min(my_wave + k * waves, groups - 1));
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const u32x4* row = sg.row(grp, r, K);
 #pragma unroll
             for (int i = 0; i < CPI; ++i) buf.w[r][i] = __builtin_nontemporal_load(row + min(lane + kWave * i, nch - 1));
         }
-        load_aux<MT, R, EPI>(p, grp, lane, first, buf.aux0, buf.aux1);
+        load_aux<MT, R, EPI>(p, grp, lane, rows, buf.aux0, buf.aux1);
     };
-    // zero the tail chunks and rows, then the fused RMSNorm of this wave's copy of the activations
-    auto prepare = [&]() {
+    // 2. the first weight group (idle LOGITS waves load a valid group and ignore it)
+    Step<R, CPI> a, b;
+    load(0, a);
+
+    // 3. while it is in flight: zero the tail chunks and rows, then the fused RMSNorm of this wave's copy
 #pragma unroll
-        for (int i = 0; i < CPI; ++i) {
-            const bool in = lane + kWave * i < nch;
+    for (int i = 0; i < CPI; ++i) {
+        const bool in = lane + kWave * i < nch;
 #pragma unroll
-            for (int m = 0; m < MT; ++m)
+        for (int m = 0; m < MT; ++m)
 #pragma unroll
-                for (int j = 0; j < CH; ++j)
-                    if (!in || m >= p.M) x[m][i][j] = 0.0f;
-        }
+            for (int j = 0; j < CH; ++j)
+                if (!in || m >= p.M) x[m][i][j] = 0.0f;
+    }
+    if constexpr (NORM) {
         if (norm) {
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
@@ -451,10 +498,28 @@ __global__ __launch_bounds__(kThreads) void gemv_reg(const dlk_gemv_params p) {
 #pragma unroll
                 for (int i = 0; i < CPI; ++i)
 #pragma unroll
-                    for (int j = 0; j < CH; ++j) x[m][i][j] = x[m][i][j] * inv * (affine ? g[NORM ? i : 0][j] : 1.0f);
+                    for (int j = 0; j < CH; j += 4) {
+                        const u32x4 w = graw[i][j / 4];
+                        float g[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+                        if (affine) {
+                            if (p.norm_bf16) {
+                                // elements j..j+3 of the chunk sit in the first load (words j/2, j/2 + 1)
+                                const u32x4 c0 = graw[i][0];
+                                const uint32_t lo = j == 0 ? c0.x : c0.z, hi = j == 0 ? c0.y : c0.w;
+                                g[0] = bf16_lo(lo); g[1] = bf16_hi(lo); g[2] = bf16_lo(hi); g[3] = bf16_hi(hi);
+                            } else {
+                                g[0] = __uint_as_float(w.x); g[1] = __uint_as_float(w.y);
+                                g[2] = __uint_as_float(w.z); g[3] = __uint_as_float(w.w);
+                            }
+                        }
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) x[m][i][j + e] = x[m][i][j + e] * inv * g[e];
+                    }
             }
         }
-    };
+    }
+
+    // 4. stream the row groups
     auto use = [&](int k, const Step<R, CPI>& buf) {
         float acc[MT][R];
 #pragma unroll
@@ -466,11 +531,10 @@ __global__ __launch_bounds__(kThreads) void gemv_reg(const dlk_gemv_params p) {
                 for (int i = 0; i < CPI; ++i) s += Traits::dot(buf.w[r][i], x[m][i]);
                 acc[m][r] = wave_sum(s) * p.acc_scale;
             }
-        finish_group<WT, MT, R, EPI>(p, sg, acc, my_wave + k * waves, lane, first, buf.aux0, buf.aux1, cand);
+        finish_group<WT, MT, R, EPI>(p, sg, acc, my_wave + k * waves, lane, rows, buf.aux0, buf.aux1, cand);
     };
-    Step<R, CPI> a, b;
-    stream_steps(my_groups, a, b, load, use, prepare);
-    finish_kernel<MT, EPI>(p, cand, lane, my_wave);
+    if (my_groups > 0) stream_steps(my_groups, a, b, load, use);
+    finish_kernel<MT, EPI>(p, cand, lane, wave_in_block);
 }
 
 // ------------------------------------------------------------------------------------------ LDS kernel
@@ -541,11 +605,13 @@ __global__ __launch_bounds__(kThreads) void gemv_lds(const dlk_gemv_params p) {
                                                              xr[i].z * inv * gr[i].z, xr[i].w * inv * gr[i].w);
     }
     lds_barrier();
-    if (jobs == 0) return;
+    if (jobs == 0) {
+        if constexpr (EPI != DLK_EPI_LOGITS) return;
+    }
 
     Candidates<MT> cand;
     init_candidates<MT, EPI>(p, cand);
-    const int64_t first = EPI == DLK_EPI_QKV ? *p.position : 0;
+    const Rows<MT> rows(p, EPI == DLK_EPI_QKV);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -560,7 +626,7 @@ __global__ __launch_bounds__(kThreads) void gemv_lds(const dlk_gemv_params p) {
 #pragma unroll
             for (int i = 0; i < CPI; ++i) buf.w[r][i] = __builtin_nontemporal_load(row + min(c0 + lane + kWave * i, nch - 1));
         }
-        load_aux<MT, R, EPI>(p, grp, lane, first, buf.aux0, buf.aux1);
+        load_aux<MT, R, EPI>(p, grp, lane, rows, buf.aux0, buf.aux1);
     };
     auto use = [&](int job, const Step<R, CPI>& buf) {
         const int c0 = (job % steps_per_group) * STEP_CHUNKS;
@@ -588,12 +654,15 @@ __global__ __launch_bounds__(kThreads) void gemv_lds(const dlk_gemv_params p) {
             v[0][r] = wave_sum(acc[r]) * p.acc_scale;
             acc[r] = 0.0f;
         }
-        finish_group<WT, MT, R, EPI>(p, sg, v, my_wave + (job / steps_per_group) * waves, lane, first, buf.aux0,
+        finish_group<WT, MT, R, EPI>(p, sg, v, my_wave + (job / steps_per_group) * waves, lane, rows, buf.aux0,
                                      buf.aux1, cand);
     };
     Step<R, CPI> a, b;
-    stream_steps(jobs, a, b, load, use, [] {});
-    finish_kernel<MT, EPI>(p, cand, lane, my_wave);
+    if (jobs > 0) {
+        load(0, a);
+        stream_steps(jobs, a, b, load, use);
+    }
+    finish_kernel<MT, EPI>(p, cand, lane, wave_in_block);
 }
 
 // ------------------------------------------------------------------------------------------ resolution
@@ -631,12 +700,14 @@ template <typename WT, int EPI, bool NORM>
 Kernel resolve_typed(const dlk_gemv_params& p, int mt) {
     const Plan plan = plan_of(p.K, sizeof(WT) == 2, EPI);
     if (plan.reg) {
+        Kernel kernel;
         switch (mt) {
-        case 1: return reg_cpi<WT, 1, EPI, NORM>(plan.cpi);
-        case 2: return reg_cpi<WT, 2, EPI, NORM>(plan.cpi);
-        case 4: return reg_cpi<WT, 4, EPI, NORM>(plan.cpi);
+        case 1: kernel = reg_cpi<WT, 1, EPI, NORM>(plan.cpi); break;
+        case 2: kernel = reg_cpi<WT, 2, EPI, NORM>(plan.cpi); break;
+        case 4: kernel = reg_cpi<WT, 4, EPI, NORM>(plan.cpi); break;
         default: return {};
         }
+        return kernel;
     }
     if (mt != 1) return {};
     return {reinterpret_cast<const void*>(&gemv_lds<WT, 2, EPI, NORM>), static_cast<size_t>(p.K) * sizeof(float)};

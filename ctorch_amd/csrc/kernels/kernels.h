@@ -82,8 +82,8 @@ typedef struct dlk_gemv_params {
     int partial_blocks;
 } dlk_gemv_params;
 
-/* Waves of the persistent launch (the LOGITS partial row length: one sampling candidate per wave); -1 when no
-   kernel fits the parameters.  Depends on the current device's CU count and the kernel's occupancy. */
+/* Work-groups of the persistent launch (the LOGITS partial row length: one sampling candidate per work-group);
+   -1 when no kernel fits the parameters.  Depends on the current device's CU count and the kernel's occupancy. */
 int dlk_gemv_blocks(const dlk_gemv_params* p);
 int dlk_gemv(const dlk_gemv_params* p, dlh_stream stream);
 
