@@ -10,8 +10,9 @@ HIP graph; exactly --steps steps are timed with HIP events on the library's comp
 untimed steps.
 
 Also reported: the b=32 decode over a 2048-token seeded K/V prefix (configs[2], "C3"), the per-kernel roofline of
-the dominant kernel (gate/up projection) from event pairs around each launch, a streaming-copy bandwidth
-reference, and the CPU oracle timed on this host (single thread) on a bounded sample of the same workload.
+the dominant kernel (gate/up projection: each layer's launch repeated back to back between two HIP events on the
+compute stream), a streaming-copy bandwidth reference, and the CPU oracle timed on this host (single thread) on
+a bounded sample of the same workload.
 """
 import argparse
 import json
@@ -25,6 +26,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per launch of the gate/up kernel: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE per dispatch, each scaled
+# by what the counter reads for this script's 1 GiB copy probe (x2.0 and x1.0); the commands and the table are in
+# the traffic summary under profiles/.  A measurement of the kernel as built, not derived from the bytes below.
+GATE_UP_TRAFFIC_BYTES = 46.37e6 + 0.045e6
 C2 = dict(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632)
 
 
@@ -95,10 +100,11 @@ def decode_b1(ct, steps, warmup):
     first = 128 + 3 + warmup
     mean_len = first + (steps - 1) / 2.0
     step_bytes = weight_bytes(C2) + kv_bytes(C2, 1, mean_len)
-    # per-kernel device time of eager single-token steps (event pair around every launch)
+    # per-kernel-class device time: each class's launches of one step (one per layer) repeated back to back
+    # between two HIP events on the compute stream (cold weights: a class's 16 layers exceed the 256 MB cache)
     pcache = ct.DecoderCache(decoder)
     lm.logits(prompt, pcache)
-    timings = lm.profile(prompt[:, -1:], pcache, 8)
+    timings = lm.profile(prompt[:, -1:], pcache, 10)
     return dict(ms=ms, step_bytes=step_bytes, timings=timings, tokens=tokens, mean_len=mean_len), decoder, lm
 
 
@@ -214,9 +220,10 @@ def main():
         "achieved_GBps": achieved,
         "frac_of_hbm_peak": achieved / HBM_PEAK_GBPS,
         "copy_GBps": copy_gbps,
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<uint16_t,1,8,DLK_EPI_SWIGLU> (gate/up + SiLU*up)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "gemv_reg<bf16, MT=1, R=2, CPI=4, SWIGLU> (RMSNorm + gate/up projection + SiLU*up)",
                      "achieved": gate_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gate_gbps / HBM_PEAK_GBPS,
-                     "traffic": None, "bytes_per_launch": gate_bytes, "avg_launch_us": gate_avg_ms * 1e3},
+                     "traffic": GATE_UP_TRAFFIC_BYTES, "bytes_per_launch": gate_bytes, "avg_launch_us": gate_avg_ms * 1e3},
         "kernels": kernels,
         "cpu_baseline": baseline,
     }

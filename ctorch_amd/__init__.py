@@ -378,11 +378,12 @@ class DecoderLM:
                                             RandomKey(key[0], key[1]), int(use_graph), C.byref(ms), C.byref(tokens)))
         return ms.value, Tensor(tokens).numpy()
 
-    def profile(self, ids: np.ndarray, cache: DecoderCache, steps: int) -> list[dict]:
+    def profile(self, ids: np.ndarray, cache: DecoderCache, rounds: int) -> list[dict]:
+        """Per kernel class: its launches of one step repeated `rounds` times back to back (HIP events)."""
         t = Tensor.from_numpy(np.ascontiguousarray(ids, np.int64), I64, device("cpu"))
         out = (KernelTiming * 32)()
         n = C.c_size_t()
-        check(lib().dl_decoder_lm_profile(self.handle, t.handle, cache.handle, steps, out, 32, C.byref(n)))
+        check(lib().dl_decoder_lm_profile(self.handle, t.handle, cache.handle, rounds, out, 32, C.byref(n)))
         return [{"name": out[i].name.decode(), "launches": out[i].launches, "total_ms": out[i].total_ms,
                  "bytes": out[i].bytes} for i in range(n.value)]
 

@@ -72,10 +72,10 @@ dl_status dl_decoder_lm_benchmark(dl_decoder_lm* lm, const dl_tensor* prompt, dl
     });
 }
 
-dl_status dl_decoder_lm_profile(dl_decoder_lm* lm, const dl_tensor* ids, dl_decoder_cache* cache, int64_t steps,
+dl_status dl_decoder_lm_profile(dl_decoder_lm* lm, const dl_tensor* ids, dl_decoder_cache* cache, int64_t rounds,
                                 dl_kernel_timing* timings, size_t capacity, size_t* count) {
     return invoke([&] {
-        auto result = require(lm, "lm").value->profile(require(ids, "ids").value, require(cache, "cache").value, steps);
+        auto result = require(lm, "lm").value->profile(require(ids, "ids").value, require(cache, "cache").value, rounds);
         const size_t n = std::min(capacity, result.size());
         for (size_t i = 0; i < n; ++i) {
             std::memset(timings[i].name, 0, sizeof(timings[i].name));

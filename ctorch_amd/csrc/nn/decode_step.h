@@ -6,6 +6,9 @@
 
 #include "nn/ops_internal.h"
 
+#include <functional>
+#include <utility>
+
 namespace dl::detail {
 
 /// Scratch of one decode chunk of `rows` = B * L activation rows.
@@ -18,13 +21,20 @@ struct DecodeWorkspace {
                 int splits, Device device);
 };
 
-/// Per-launch timing hook (profiling); called with a kernel-class name and the algorithmic bytes before and
-/// after each launch.  Null in normal operation.
+/// Launch hook for profiling (null in normal operation).  Every launch of a step is handed over as a closure
+/// with its kernel-class name and algorithmic HBM bytes: `fn(false)` issues the step's own launch, `fn(true)`
+/// issues the identical launch again without side effects on cache lengths (a timing repeat).
 struct LaunchObserver {
     virtual ~LaunchObserver() = default;
-    virtual void before(const char* name, double bytes) = 0;
-    virtual void after() = 0;
+    virtual void launch(const char* name, double bytes, std::function<void(bool repeat)> fn) = 0;
 };
+
+/// Issues one launch: directly, or through the observer.
+template <typename F>
+void issue(LaunchObserver* observer, const char* name, double bytes, F&& fn) {
+    if (observer) observer->launch(name, bytes, std::function<void(bool)>(std::forward<F>(fn)));
+    else fn(false);
+}
 
 /// Runs one layer on x_in [B*L, d] f32 (device) and writes x_out (may alias x_in).  The cache must be
 /// reserved; its device length is advanced by L on the device, and on the host by the caller.

@@ -61,15 +61,19 @@ void DecoderLM::forward_chunk(const Index* ids, Index batch, Index length, std::
     }
     if (!logits_.defined() || logits_.size(0) != batch) logits_ = empty_tensor({batch, V}, DType::f32, device);
     float* x = static_cast<float*>(mutable_data(x_));
-    auto observe = [&](const char* name, double bytes) { if (observer) observer->before(name, bytes); };
-    auto done = [&]() { if (observer) observer->after(); };
+    GpuContext* context = context_;
 
     if (ids) {
-        observe("embedding", static_cast<double>(rows * d) * static_cast<double>(element_size(embedding_->weight().dtype())));
-        hip_check(dlk_embedding(ids, rows, embedding_->weight().data<void>(), dlk_dtype(embedding_->weight().dtype()),
-                                embedding_->weight().size(0), d, x, DLK_F32, context_->error_flag, context_->stream),
-                  "embedding");
-        done();
+        const void* table = embedding_->weight().data<void>();
+        const int table_dtype = dlk_dtype(embedding_->weight().dtype());
+        const Index vocabulary = embedding_->weight().size(0);
+        issue(observer, "embedding",
+              static_cast<double>(rows * d) * static_cast<double>(element_size(embedding_->weight().dtype())),
+              [=](bool) {
+                  hip_check(dlk_embedding(ids, rows, table, table_dtype, vocabulary, d, x, DLK_F32, context->error_flag,
+                                          context->stream),
+                            "embedding");
+              });
     }
 
     const auto& first = decoder_->layer(0).attention();
@@ -115,20 +119,23 @@ void DecoderLM::forward_chunk(const Index* ids, Index batch, Index length, std::
         p.partial = static_cast<dlk_sample_partial*>(mutable_data(partial_));
         p.partial_blocks = blocks;
     }
-    observe("lm_head", static_cast<double>(V * d) * (hb ? 2 : 4));
-    hip_check(dlk_gemv(&p, context_->stream), "LM head");
-    done();
+    issue(observer, "lm_head", static_cast<double>(V * d) * (hb ? 2 : 4),
+          [p, context](bool) { hip_check(dlk_gemv(&p, context->stream), "LM head"); });
     if (sample_mode > 0) {
-        observe("sample_finalize", 0.0);
         // the sampled ids are fed back: their embedding rows become the next step's input x[0:B]
-        hip_check(dlk_sample_finalize(static_cast<const dlk_sample_partial*>(partial_.data<void>()), batch, blocks_,
-                                      nullptr, static_cast<Index*>(mutable_data(next_ids_)),
-                                      tokens_.defined() ? static_cast<Index*>(mutable_data(tokens_)) : nullptr,
-                                      token_columns_, static_cast<Index*>(mutable_data(step_)),
-                                      embedding_->weight().data<void>(), dlk_dtype(embedding_->weight().dtype()), d, x,
-                                      context_->stream),
-                  "sample");
-        done();
+        const auto* partial = static_cast<const dlk_sample_partial*>(partial_.data<void>());
+        Index* next = static_cast<Index*>(mutable_data(next_ids_));
+        Index* tokens = tokens_.defined() ? static_cast<Index*>(mutable_data(tokens_)) : nullptr;
+        Index* step = static_cast<Index*>(mutable_data(step_));
+        const void* table = embedding_->weight().data<void>();
+        const int table_dtype = dlk_dtype(embedding_->weight().dtype());
+        const int blocks = blocks_;
+        const Index columns = token_columns_;
+        issue(observer, "sample_finalize", 0.0, [=](bool) {
+            hip_check(dlk_sample_finalize(partial, batch, blocks, nullptr, next, tokens, columns, step, table,
+                                          table_dtype, d, x, context->stream),
+                      "sample");
+        });
     }
 }
 
@@ -252,59 +259,72 @@ double DecoderLM::benchmark(const Tensor& prompt, std::span<nn::KVCache> cache, 
 }
 
 namespace {
-struct EventObserver final : LaunchObserver {
-    struct Pending {
+// Records every launch of a step (and issues it); the profile then repeats each kernel class on its own.
+struct ReplayObserver final : LaunchObserver {
+    struct Entry {
         std::string name;
         double bytes;
-        dlh_event start, stop;
+        std::function<void(bool)> fn;
     };
-    dlh_stream stream;
-    std::vector<Pending> pending;
-    explicit EventObserver(dlh_stream s) : stream(s) {}
-    ~EventObserver() override {
-        for (auto& p : pending) {
-            (void)dlh_event_destroy(p.start);
-            (void)dlh_event_destroy(p.stop);
-        }
+    std::vector<Entry> entries;
+    void launch(const char* name, double bytes, std::function<void(bool)> fn) override {
+        fn(false);
+        entries.push_back({name, bytes, std::move(fn)});
     }
-    void before(const char* name, double bytes) override {
-        Pending p{name, bytes, nullptr, nullptr};
-        hip_check(dlh_event_create(&p.start), "event");
-        hip_check(dlh_event_create(&p.stop), "event");
-        hip_check(dlh_event_record(p.start, stream), "event record");
-        pending.push_back(p);
-    }
-    void after() override { hip_check(dlh_event_record(pending.back().stop, stream), "event record"); }
 };
 } // namespace
 
-std::vector<KernelTiming> DecoderLM::profile(const Tensor& ids, std::span<nn::KVCache> cache, Index steps) {
+std::vector<KernelTiming> DecoderLM::profile(const Tensor& ids, std::span<nn::KVCache> cache, Index rounds) {
     if (ids.ndim() != 2 || ids.dtype() != DType::i64 || ids.size(1) != 1)
         throw std::invalid_argument("profile ids must be i64 [B, 1]");
+    if (rounds <= 0) throw std::invalid_argument("profile needs rounds > 0");
     const Index B = ids.size(0);
-    check_caches(cache, B, steps);
+    check_caches(cache, B, 2); // the step's own token plus the slot its QKV repeats write
     const Device device = embedding_->weight().device();
     Tensor dev_ids = ids.to(device).contiguous();
     step_ = zeros({1}, {.dtype = DType::i64, .device = device});
     next_ids_ = dev_ids.clone();
     tokens_ = Tensor();
-    EventObserver observer(context_->stream);
-    for (Index s = 0; s < steps; ++s)
-        forward_chunk(s == 0 ? next_ids_.data<Index>() : nullptr, B, 1, cache, 1, 0.0, {0, 0}, false, &observer);
+    ReplayObserver observer;
+    forward_chunk(next_ids_.data<Index>(), B, 1, cache, 1, 0.0, {0, 0}, false, &observer);
     hip_check(dlh_stream_synchronize(context_->stream), "profile");
+
+    // each class: all of its launches of the step (one per layer), `rounds` times back to back between two events
     std::vector<KernelTiming> out;
-    for (const auto& p : observer.pending) {
-        float ms = 0.0f;
-        hip_check(dlh_event_elapsed(p.start, p.stop, &ms), "event elapsed");
-        auto it = std::find_if(out.begin(), out.end(), [&](const KernelTiming& k) { return k.name == p.name; });
-        if (it == out.end()) {
-            out.push_back({p.name, 0, 0.0, 0.0});
-            it = out.end() - 1;
+    dlh_event start = nullptr, stop = nullptr;
+    hip_check(dlh_event_create(&start), "event");
+    hip_check(dlh_event_create(&stop), "event");
+    try {
+        for (const auto& first : observer.entries) {
+            if (std::any_of(out.begin(), out.end(), [&](const KernelTiming& k) { return k.name == first.name; }))
+                continue;
+            KernelTiming timing{first.name, 0, 0.0, 0.0};
+            for (const auto& e : observer.entries)
+                if (e.name == first.name) e.fn(true); // warm-up round
+            hip_check(dlh_event_record(start, context_->stream), "event record");
+            for (Index r = 0; r < rounds; ++r)
+                for (const auto& e : observer.entries)
+                    if (e.name == first.name) {
+                        e.fn(true);
+                        timing.launches += 1;
+                        timing.bytes += e.bytes;
+                    }
+            hip_check(dlh_event_record(stop, context_->stream), "event record");
+            hip_check(dlh_stream_synchronize(context_->stream), "profile");
+            float ms = 0.0f;
+            hip_check(dlh_event_elapsed(start, stop, &ms), "event elapsed");
+            timing.total_ms = ms;
+            out.push_back(timing);
         }
-        it->launches += 1;
-        it->total_ms += ms;
-        it->bytes += p.bytes;
+    } catch (...) {
+        (void)dlh_event_destroy(start);
+        (void)dlh_event_destroy(stop);
+        throw;
     }
+    (void)dlh_event_destroy(start);
+    (void)dlh_event_destroy(stop);
+    for (auto& c : cache) c.truncate(c.length()); // repeats never moved the lengths; rewrite them on the device
+    check_device_errors(device, "embedding");
     return out;
 }
 

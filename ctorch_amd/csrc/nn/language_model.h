@@ -27,7 +27,7 @@ public:
     /// Prompt then `steps` sampled tokens; returns tokens [B, steps] and the last logits [B, V].
     std::pair<Tensor, Tensor> generate(const Tensor& prompt, std::span<nn::KVCache> cache, Index steps,
                                        double temperature, RandomKey key, bool use_graph);
-    std::vector<KernelTiming> profile(const Tensor& ids, std::span<nn::KVCache> cache, Index steps);
+    std::vector<KernelTiming> profile(const Tensor& ids, std::span<nn::KVCache> cache, Index rounds);
     /// Prompt, then warmup + timed single-token steps; the last `timed` steps are bracketed by HIP events on
     /// the compute stream (after a synchronize) and their device time is returned in milliseconds.
     double benchmark(const Tensor& prompt, std::span<nn::KVCache> cache, Index warmup, Index timed,

@@ -47,10 +47,13 @@ DL_API dl_status dl_decoder_lm_benchmark(dl_decoder_lm* lm, const dl_tensor* pro
     int64_t warmup, int64_t timed, double temperature, dl_random_key key, int32_t use_graph, double* milliseconds,
     dl_tensor** tokens);
 
-/* Per-kernel-class device time of single-token steps, measured with a HIP event pair around every launch
- * on the compute stream.  `steps` decode steps are run eagerly from ids [B, 1] (greedy), and for each
- * kernel class the launch count, summed duration and algorithmic HBM bytes (weights + KV read/written,
- * counted once) are written to `timings` (up to `capacity` entries; *count receives the number used). */
+/* Per-kernel-class device time of a single-token step.  One greedy step is run eagerly from ids [B, 1]
+ * (appending one position to `cache`, which needs room for two); then each kernel class is timed on its
+ * own: all of its launches of that step (one per layer) are issued again, complete and unchanged except
+ * that they leave the cache lengths alone, `rounds` times back to back between two HIP events on the
+ * compute stream.  For each class the launch count, summed duration and algorithmic HBM bytes (weights +
+ * KV read/written, counted once per launch) are written to `timings` (up to `capacity` entries; *count
+ * receives the number used). */
 typedef struct dl_kernel_timing {
     char name[48];
     int64_t launches;
@@ -58,7 +61,7 @@ typedef struct dl_kernel_timing {
     double bytes;
 } dl_kernel_timing;
 DL_API dl_status dl_decoder_lm_profile(dl_decoder_lm* lm, const dl_tensor* ids, dl_decoder_cache* cache,
-    int64_t steps, dl_kernel_timing* timings, size_t capacity, size_t* count);
+    int64_t rounds, dl_kernel_timing* timings, size_t capacity, size_t* count);
 
 /* One index per row of logits [B, V] (f32 or bf16, GPU): temperature <= 0 is the reference argmax rule;
  * otherwise Gumbel-max argmax_i(logit_i / T + g_i), g = -log(-log u), u from Philox(key, b*V + i) on (0, 1),

@@ -153,6 +153,14 @@ def test_operators_match_the_oracle():
         vv = rng.standard_normal((2, 2, S, 64)).astype(np.float32)
         y = ct.grouped_query_attention(G(qq), G(kk), G(vv)).numpy()
         assert np.max(np.abs(y - oracle.attention(qq, kk, vv, -1))) <= 1e-5
+    # one position over bf16 K/V: the decode kernel, with 1..3 key chunks of 256 merged by the combine pass
+    for S, hd, heads in ((1, 64, 8), (64, 64, 8), (200, 64, 8), (257, 64, 8), (700, 64, 16), (300, 128, 8)):
+        qq = rng.standard_normal((2, heads, 1, hd)).astype(np.float32)
+        kb = oracle.bf16_encode(rng.standard_normal((2, 2, S, hd)).astype(np.float32))
+        vb = oracle.bf16_encode(rng.standard_normal((2, 2, S, hd)).astype(np.float32))
+        y = ct.grouped_query_attention(G(qq), G(kb, ct.BF16), G(vb, ct.BF16)).numpy()
+        want = oracle.attention(qq, oracle.bf16_decode(kb), oracle.bf16_decode(vb), -1)
+        assert np.max(np.abs(y - want)) <= 2e-5, (S, hd, heads)
 
 
 # ------------------------------------------------------------------------------------------ seeded prefix
@@ -176,6 +184,33 @@ def test_batched_decode_over_a_seeded_prefix():
         got = gpu.logits(ids, gc)
         assert np.max(np.abs(got - want)) <= 2e-2, step
         ids = want.argmax(-1).reshape(B, 1)
+
+
+def test_decode_across_key_chunks_merges_in_kernel():
+    say("case: B=2 decode over a 600-token prefix, head dim 64, 4 query heads per KV head (3 key chunks)")
+    cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=512, context=640,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(43, 0), scale=0.05)
+    B, P, hd = 2, 600, cfg.head_dim
+    rc, gc = ref.make_cache(B), gpu.cache()
+    for layer in range(cfg.layers):
+        k = oracle.randn(oracle.fold_in((79, 0), 2 * layer), B * 2 * P * hd).reshape(B, 2, P, hd)
+        v = oracle.randn(oracle.fold_in((79, 0), 2 * layer + 1), B * 2 * P * hd).reshape(B, 2, P, hd)
+        kb, vb = oracle.bf16_encode(k), oracle.bf16_encode(v)
+        gc.append(layer, ct.Tensor.from_numpy(kb, ct.BF16, GPU), ct.Tensor.from_numpy(vb, ct.BF16, GPU))
+        rc.fill(layer, P, oracle.bf16_decode(kb), oracle.bf16_decode(vb))
+    ids = oracle.random_ids((80, 0), B, cfg.vocab).reshape(B, 1)
+    for step in range(3):  # eager steps: split count from the live length, merged by the last chunk to finish
+        want = ref.logits(ids, rc)[:, -1]
+        got = gpu.logits(ids, gc)
+        assert np.max(np.abs(got - want)) <= 2e-2, step
+        ids = want.argmax(-1).reshape(B, 1)
+    # the graph-replayed token loop (splits sized for the capacity, chunks past the length idle) equals eager
+    gc.truncate(P)
+    t1, l1 = gpu.generate(ids, 12, 0.0, (0, 0), use_graph=True, cache=gc)
+    gc.truncate(P)
+    t2, l2 = gpu.generate(ids, 12, 0.0, (0, 0), use_graph=False, cache=gc)
+    assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
 
 
 # ------------------------------------------------------------------------------------------ C2 shape
