@@ -6,10 +6,13 @@
 // prefetched into registers while the current one is used) and staged in LDS with a padded row stride, so
 // every query head of the group reuses them.  Scores use one lane per key, softmax is online (running max and
 // sum per row, wave64 reductions), P*V uses one lane per head-dim column.  With one split the work-group
-// writes the normalised output; otherwise it writes (o, max, sum) partials that attention_combine merges.
+// writes the normalised output; otherwise it writes (o, max, sum) partials that attention_combine merges in a
+// second launch (the kernel boundary orders them: no device-scope fence, whose L2 write-back across the XCDs
+// costs microseconds per work-group).
 #include "kernels/device_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace dlk {
 namespace {
@@ -17,8 +20,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kRowsMax = 16;
-constexpr int kDecodeChunk = kWaves * kWave; // keys per work-group of the decode kernel
-static_assert(kDecodeChunk == DLK_DECODE_CHUNK, "decode chunk");
+constexpr int kDecodeChunkMax = 16 * kWave; // keys per work-group of the decode kernel, at most
+static_assert(kDecodeChunkMax == DLK_DECODE_CHUNK_MAX, "decode chunk");
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename KT> struct KvTraits;
@@ -168,8 +171,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const dlk_attention
         }
     }
 
-    // write results
-    const bool merge_here = p.splits > 1 && p.merge_counters;
+    // write results: the normalised output with one split, else (o, max, sum) partials for the combine pass
 #pragma unroll
     for (int j = 0; j < RPW; ++j) {
         const int r = wave + j * kWaves;
@@ -197,53 +199,6 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const dlk_attention
             }
         }
     }
-    if (!merge_here) return;
-
-    // last-arriver merge: publish this split's partials, count arrivals; the work-group that completes the
-    // count merges all splits of its rows (fixed split order, so the result is deterministic) and resets the
-    // counter for the next launch.  Nothing waits on another work-group.
-    __shared__ int last;
-    __threadfence();
-    __syncthreads();
-    int* counter = p.merge_counters + (static_cast<int64_t>(blockIdx.z) * gridDim.y + blockIdx.y);
-    if (t == 0) last = atomicAdd(counter, 1) == p.splits - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-#pragma unroll
-    for (int j = 0; j < RPW; ++j) {
-        const int r = wave + j * kWaves;
-        if (r >= rows) break;
-        const int l = row_l(r), h = row_h(r);
-        const int64_t prow = (static_cast<int64_t>(b) * p.H + h) * p.L + l;
-        const float* ml = p.partial_ml + prow * p.splits * 2;
-        float maximum = -INFINITY;
-        for (int s = 0; s < p.splits; ++s) maximum = fmaxf(maximum, ml[2 * s]);
-        float total = 0.0f, acc[DCOLS];
-#pragma unroll
-        for (int c = 0; c < DCOLS; ++c) acc[c] = 0.0f;
-        for (int s = 0; s < p.splits; ++s) {
-            const float ms = ml[2 * s], ls = ml[2 * s + 1];
-            if (ls <= 0.0f || ms == -INFINITY) continue;
-            const float w = expf(ms - maximum);
-            total += w * ls;
-            const float* o = p.partial_o + (prow * p.splits + s) * HD;
-#pragma unroll
-            for (int c = 0; c < DCOLS; ++c) {
-                const int d = lane + c * kWave;
-                if (d < HD) acc[c] += w * o[d];
-            }
-        }
-        // o * (1/l): the rounding of the single-split path, so a launch whose extra splits are empty matches it
-        const float inv = total > 0.0f ? 1.0f / total : 0.0f;
-        const int64_t m = static_cast<int64_t>(b) * p.L + l;
-#pragma unroll
-        for (int c = 0; c < DCOLS; ++c) {
-            const int d = lane + c * kWave;
-            if (d < HD) p.out[m * p.ldo + static_cast<int64_t>(h) * HD + d] = acc[c] * inv;
-        }
-    }
-    if (t == 0) *counter = 0;
 }
 
 // One wave per (b, h, l) row: merges the split partials with the usual max-rescaled weights.
@@ -281,22 +236,23 @@ __global__ __launch_bounds__(kWave) void attention_combine(const dlk_attention_p
 }
 
 // ------------------------------------------------------------------------------------------ decode
-// One new position per sequence (L = 1) over bf16 K/V, G = H/KV query heads per KV head.  A work-group takes
-// one (sequence, KV head, key chunk of <= 256 keys); each wave one 64-key tile of the chunk, loaded straight
-// into registers when the kernel starts (no dependency precedes them): the K rows with one lane per key for
-// the scores, the V rows with one lane per pair of head-dim columns for P*V.  The scaled q rows are broadcast
-// from LDS.  Each wave normalises its tile on its own (max, exp, sum); the four waves merge through LDS.  Only
-// chunks that hold keys take part: with one such chunk the work-group writes the output itself, otherwise the
-// last of them to finish merges the partials of all (fixed order) and resets its counter.
+// One new position per sequence (L = 1) over bf16 K/V, G = H/KV query heads per KV head.  A work-group of W
+// waves takes one (sequence, KV head, key chunk of 64 W keys); each wave one 64-key tile of the chunk, loaded
+// straight into registers when the kernel starts (no dependency precedes them): the K rows with one lane per
+// key for the scores, the V rows with one lane per pair of head-dim columns for P*V.  The scaled q rows are
+// broadcast from LDS.  Each wave normalises its tile on its own (max, exp, sum); the W waves merge through
+// LDS.  A single chunk writes the output; with several, each writes (o, max, sum) partials (empty ones a
+// zero weight) and attention_combine merges them in fixed order in the next launch.
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int HD, int G>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_decode(
+template <int HD, int G, int W>
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_decode(
     const dlk_attention_params p) {
+    constexpr int kThreads = W * kWave;
     constexpr int KCH = HD * 2 / 16;  // 16-byte chunks of a K row
     constexpr int DL = HD / 2;        // lanes per V row (two bf16 columns per lane)
     constexpr int KP = kWave / DL;    // keys per V load instruction
@@ -304,10 +260,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
     constexpr int QN = (G * HD + kThreads - 1) / kThreads;
     static_assert(DL <= kWave && kWave % DL == 0, "a V row must fit one wave");
     __shared__ float q_s[G][HD];
-    __shared__ float p_s[kWaves][kWave][G];
-    __shared__ float m_s[kWaves][G], l_s[kWaves][G];
-    __shared__ float o_s[kWaves][G][HD];
-    __shared__ int last;
+    __shared__ float p_s[W][kWave][G];
+    __shared__ float m_s[W][G], l_s[W][G];
+    __shared__ float o_s[W][G][HD];
 
     const int t = threadIdx.x, lane = t % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
@@ -317,12 +272,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
     const int64_t first = p.position ? *p.position : p.first_host;
     const int64_t S = first + 1;
     const int active = static_cast<int>((S + p.chunk - 1) / p.chunk);
-    const bool gather = p.splits > 1 && !p.merge_counters; // the combine pass (or the caller) reads every slot
-    const bool direct = p.splits == 1 || (active == 1 && !gather);
 
     if (split >= active) {
-        // no keys here: the combine pass still reads this slot
-        if (gather && t < G) {
+        // no keys here: the combine pass gives this slot zero weight
+        if (t < G) {
             const int64_t slot = (static_cast<int64_t>(b) * p.H + kvh * G + t) * p.splits + split;
             p.partial_ml[slot * 2] = -INFINITY;
             p.partial_ml[slot * 2 + 1] = 0.0f;
@@ -471,7 +424,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
             o[g][1] += __shfl_xor(o[g][1], off, kWave);
         }
 
-    // merge the four waves
+    // merge the W waves
     if (lane == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -491,16 +444,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
         const int g = idx / HD, d = idx % HD, h = kvh * G + g;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m_s[w][g]);
+        for (int w = 0; w < W; ++w) M = fmaxf(M, m_s[w][g]);
         float L = 0.0f, O = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < W; ++w) {
             if (m_s[w][g] == -INFINITY) continue;
             const float wt = expf(m_s[w][g] - M);
             L += wt * l_s[w][g];
             O += wt * o_s[w][g][d];
         }
-        if (direct) {
+        if (p.splits == 1) {
             p.out[static_cast<int64_t>(b) * p.ldo + static_cast<int64_t>(h) * HD + d] = O * (1.0f / L);
         } else {
             const int64_t slot = (static_cast<int64_t>(b) * p.H + h) * p.splits + split;
@@ -511,63 +464,62 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
             }
         }
     }
-    if (direct || gather) return;
+}
 
-    // last-arriver merge over the chunks that hold keys
-    __threadfence();
-    __syncthreads();
-    int* counter = p.merge_counters + bk;
-    if (t == 0) last = atomicAdd(counter, 1) == active - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    for (int idx = t; idx < G * HD; idx += kThreads) {
-        const int g = idx / HD, d = idx % HD, h = kvh * G + g;
-        const int64_t prow = static_cast<int64_t>(b) * p.H + h;
-        const float* ml = p.partial_ml + prow * p.splits * 2;
-        float M = -INFINITY;
-        for (int s = 0; s < active; ++s) M = fmaxf(M, ml[2 * s]);
-        float total = 0.0f, acc = 0.0f;
-        for (int s = 0; s < active; ++s) {
-            const float ms = ml[2 * s], ls = ml[2 * s + 1];
-            if (ls <= 0.0f || ms == -INFINITY) continue;
-            const float w = expf(ms - M);
-            total += w * ls;
-            acc += w * p.partial_o[(prow * p.splits + s) * HD + d];
+/// Widest work-group (waves) each decode variant runs without register spills: a wave may hold 512 / (W / 4)
+/// registers, and the variants need ~90-210 (HD 64) or ~155-335 (HD 128).
+constexpr int decode_waves_max(int hd, int g) {
+    return hd == 64 ? (g <= 2 ? 16 : 8) : (g <= 2 ? 8 : 4);
+}
+
+template <int HD, int W>
+int launch_decode_w(const dlk_attention_params& p, hipStream_t stream) {
+    const dim3 grid(p.splits, p.B * p.KV), block(W * kWave);
+    auto go = [&](auto g) {
+        constexpr int G = decltype(g)::value;
+        if constexpr (W <= decode_waves_max(HD, G) && !(HD == 128 && G > 4)) {
+            hipLaunchKernelGGL((attention_decode<HD, G, W>), grid, block, 0, stream, p);
+            return static_cast<int>(hipGetLastError());
         }
-        p.out[static_cast<int64_t>(b) * p.ldo + static_cast<int64_t>(h) * HD + d] = acc * (1.0f / total);
+        return static_cast<int>(hipErrorInvalidValue);
+    };
+    switch (p.H / p.KV) {
+    case 1: return go(std::integral_constant<int, 1>{});
+    case 2: return go(std::integral_constant<int, 2>{});
+    case 4: return go(std::integral_constant<int, 4>{});
+    case 8: return go(std::integral_constant<int, 8>{});
+    default: return static_cast<int>(hipErrorInvalidValue);
     }
-    if (t == 0) *counter = 0;
 }
 
 template <int HD>
 int launch_decode(const dlk_attention_params& p, hipStream_t stream) {
-    const dim3 grid(p.splits, p.B * p.KV);
-    switch (p.H / p.KV) {
-    case 1: hipLaunchKernelGGL((attention_decode<HD, 1>), grid, dim3(kThreads), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((attention_decode<HD, 2>), grid, dim3(kThreads), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((attention_decode<HD, 4>), grid, dim3(kThreads), 0, stream, p); break;
-    case 8:
-        if constexpr (HD == 64) {
-            hipLaunchKernelGGL((attention_decode<HD, 8>), grid, dim3(kThreads), 0, stream, p);
-            break;
-        }
-        return static_cast<int>(hipErrorInvalidValue);
+    int status = 0;
+    switch (p.chunk / kWave) {
+    case 4: status = launch_decode_w<HD, 4>(p, stream); break;
+    case 8: status = launch_decode_w<HD, 8>(p, stream); break;
+    case 16: status = launch_decode_w<HD, 16>(p, stream); break;
     default: return static_cast<int>(hipErrorInvalidValue);
     }
-    int status = static_cast<int>(hipGetLastError());
-    if (status != 0 || p.splits == 1 || p.partials_only || p.merge_counters) return status;
+    if (status != 0 || p.splits == 1 || p.partials_only) return status;
     const int64_t combine_rows = static_cast<int64_t>(p.B) * p.H;
     hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kWave), 0, stream, p);
     return static_cast<int>(hipGetLastError());
 }
 
 /// The decode kernel serves one new position over bf16 K/V with HD 64 (G in {1, 2, 4, 8}) or 128 (G <= 4) and
-/// chunks of at most four 64-key tiles.
+/// chunks of 4, 8 or 16 64-key tiles (one per wave).
+int decode_chunk_max(int heads, int kv_heads, int hd, int kv_bf16) {
+    if (!kv_bf16 || kv_heads <= 0 || heads % kv_heads != 0 || (hd != 64 && hd != 128)) return 0;
+    const int G = heads / kv_heads;
+    if (!(G == 1 || G == 2 || G == 4 || (G == 8 && hd == 64))) return 0;
+    return decode_waves_max(hd, G) * kWave;
+}
+
 bool decode_path(const dlk_attention_params& p) {
-    const int G = p.H / p.KV;
-    return p.kv_bf16 && p.L == 1 && (p.hd == 64 || p.hd == 128) && (G == 1 || G == 2 || G == 4 || (G == 8 && p.hd == 64)) &&
-           p.chunk <= kDecodeChunk && p.chunk % kWave == 0;
+    const int most = decode_chunk_max(p.H, p.KV, p.hd, p.kv_bf16);
+    return p.L == 1 && most > 0 && p.chunk <= most &&
+           (p.chunk == 4 * kWave || p.chunk == 8 * kWave || p.chunk == 16 * kWave);
 }
 
 template <typename KT, int HD>
@@ -579,7 +531,7 @@ int launch(const dlk_attention_params& p, hipStream_t stream) {
     dim3 grid(p.splits, row_blocks, p.B * p.KV);
     hipLaunchKernelGGL((attention_kernel<KT, HD, T>), grid, dim3(kThreads), 0, stream, p);
     int status = static_cast<int>(hipGetLastError());
-    if (status != 0 || p.splits == 1 || p.partials_only || p.merge_counters) return status;
+    if (status != 0 || p.splits == 1 || p.partials_only) return status;
     const int64_t combine_rows = static_cast<int64_t>(p.B) * p.H * p.L;
     hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kWave), 0, stream, p);
     return static_cast<int>(hipGetLastError());
@@ -588,8 +540,8 @@ int launch(const dlk_attention_params& p, hipStream_t stream) {
 } // namespace
 } // namespace dlk
 
-extern "C" int dlk_attention_row_blocks(int heads, int kv_heads, int length) {
-    return (heads / kv_heads * length + dlk::kRowsMax - 1) / dlk::kRowsMax;
+extern "C" int dlk_attention_decode_chunk(int heads, int kv_heads, int head_dim, int kv_bf16) {
+    return dlk::decode_chunk_max(heads, kv_heads, head_dim, kv_bf16);
 }
 
 extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stream_handle) {

@@ -33,6 +33,8 @@ constexpr int kLdsBytes = 60 * 1024;  // staged activation row of the fallback k
 constexpr int kLdsSteps = 4;          // chunks per lane per step in the fallback kernel
 constexpr int kLdsXL = 15;            // float4 activation loads per thread in the fallback (K <= 15360)
 constexpr int kRegBudget = 192;       // VGPRs for activations + two weight buffers in the register kernel
+constexpr int kRegBudgetRows = 128;   // the same, for launches of more than one activation row (the compiler's
+                                      // own temporaries roughly double it; past 256 it spills to AGPR moves)
 constexpr int kOutOfRange = 0x7fffff00; // buffer offset past any range: the load returns zeros, touches nothing
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -40,7 +42,7 @@ constexpr bool pair_epilogue(int epi) { return epi == DLK_EPI_QKV || epi == DLK_
 /// rows per group: RoPE pairs and gate/up pairs need two; otherwise two while rows are short
 constexpr int group_rows(int epi, int cpi) { return pair_epilogue(epi) || cpi <= 4 ? 2 : 1; }
 constexpr bool reg_fits(int mt, int cpi, int chunk, int epi) {
-    return mt * cpi * chunk + 2 * group_rows(epi, cpi) * cpi * 4 <= kRegBudget;
+    return mt * cpi * chunk + 2 * group_rows(epi, cpi) * cpi * 4 <= (mt == 1 ? kRegBudget : kRegBudgetRows);
 }
 
 /// How one launch is shaped (host side): kernel kind, chunks per lane, rows per group, activation rows.

@@ -113,16 +113,14 @@ typedef struct dlk_attention_params {
     int chunk;               /* keys per split (multiple of the tile) */
     float* partial_o;        /* [B*H*L, splits, hd] */
     float* partial_ml;       /* [B*H*L, splits, 2] */
-    int partials_only;       /* splits > 1 without merge_counters: leave the merge to the caller */
-    int* merge_counters;     /* splits > 1: [B*KV*row_blocks] zeroed counters; the last split work-group of
-                              * each (b, kv head, row block) merges the partials and resets its counter */
+    int partials_only;       /* splits > 1: leave the merge of the partials to the caller (no combine launch) */
 } dlk_attention_params;
 
-/* Keys per split that the one-position decode kernel takes (bf16 K/V, L = 1): chunk <= this uses it. */
-#define DLK_DECODE_CHUNK 256
+/* Keys per split of the one-position decode kernel (bf16 K/V, L = 1): 256, 512 or 1024 (64 per wave). */
+#define DLK_DECODE_CHUNK_MAX 1024
+/* The widest decode chunk for this head layout (0 when the decode kernel does not apply). */
+int dlk_attention_decode_chunk(int heads, int kv_heads, int head_dim, int kv_bf16);
 
-/* Query-row blocks of one (b, kv head) in dlk_attention (merge_counters has B*KV*blocks entries). */
-int dlk_attention_row_blocks(int heads, int kv_heads, int length);
 
 int dlk_attention(const dlk_attention_params* p, dlh_stream stream);
 

@@ -43,15 +43,6 @@ void DecodeWorkspace::ensure(const TransformerDecoderLayer& layer, Index n, Inde
         lora_value = empty_tensor({n, va->rank()}, DType::f32, device);
 }
 
-int* DecodeWorkspace::merge_counters(Index count, Device device, GpuContext& context) {
-    if (!counters.defined() || counters.numel() * 2 < count || !(counters.device() == device)) {
-        // zero once; every attention launch leaves its counters at zero again
-        counters = empty_tensor({(count + 1) / 2}, DType::i64, device);
-        hip_check(dlk_fill(mutable_data(counters), DLK_I64, counters.numel(), 0.0, context.stream), "merge counters");
-    }
-    return static_cast<int*>(mutable_data(counters));
-}
-
 namespace {
 const void* norm_data(const nn::RMSNorm& norm, int& bf16) {
     const auto& w = norm.weight();
@@ -170,10 +161,6 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         if (splits > 1) {
             a.partial_o = static_cast<float*>(mutable_data(ws.partial_o));
             a.partial_ml = static_cast<float*>(mutable_data(ws.partial_ml));
-            a.merge_counters = ws.merge_counters(batch * KV * dlk_attention_row_blocks(static_cast<int>(H),
-                                                                                       static_cast<int>(KV),
-                                                                                       static_cast<int>(length)),
-                                                 device, context);
         }
         const double bytes = 2.0 * kv_bytes_per * static_cast<double>(cache.length() + length);
         issue(observer, "attention", bytes,

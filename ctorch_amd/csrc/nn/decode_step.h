@@ -1,6 +1,6 @@
 // The fused per-layer decode step shared by TransformerDecoderLayer::decode, TransformerDecoder::decode and the
 // on-device token loop.  One layer is five launches: QKV projection (RMSNorm prologue, RoPE + KV-append
-// epilogue), split-K attention (+ combine), output projection (+ residual, advances the device length),
+// epilogue), attention (+ a combine launch when the keys are split), output projection (+ residual, advances the device length),
 // gate/up projection (RMSNorm prologue, SiLU*up epilogue), down projection (+ residual).
 #pragma once
 
@@ -14,9 +14,7 @@ namespace dl::detail {
 /// Scratch of one decode chunk of `rows` = B * L activation rows.
 struct DecodeWorkspace {
     Index rows = 0, splits_capacity = 0;
-    Tensor q, attention, hidden, activation, partial_o, partial_ml, lora_query, lora_value, counters;
-    /// Zeroed i32 split-merge counters for the attention kernel (at least `count`).
-    int* merge_counters(Index count, Device device, GpuContext& context);
+    Tensor q, attention, hidden, activation, partial_o, partial_ml, lora_query, lora_value;
     void ensure(const nn::TransformerDecoderLayer& layer, Index rows, Index heads_total, Index hidden_features,
                 int splits, Device device);
 };

@@ -258,7 +258,7 @@ Tensor GroupedQueryAttention::run(const Tensor& input, KVCache* cache) {
     a.causal = 1;
     a.out = static_cast<float*>(mutable_data(attended));
     a.ldo = d;
-    attention_split(B, kv_heads_, L, offset + L, a.splits, a.chunk);
+    attention_split(B, heads_, kv_heads_, hd, a.kv_bf16 != 0, L, offset + L, a.splits, a.chunk);
     Tensor po, pml;
     if (a.splits > 1) {
         po = empty_tensor({B * heads_ * L, a.splits, hd}, DType::f32, input.device());
@@ -310,7 +310,8 @@ Tensor TransformerDecoderLayer::decode(const Tensor& input, KVCache& cache) {
     Tensor out = empty_tensor({B, L, d}, DType::f32, input.device());
     DecodeWorkspace ws;
     int splits = 1, chunk = 64;
-    attention_split(B, attention_->kv_heads(), L, cache.length() + L, splits, chunk);
+    attention_split(B, attention_->heads(), attention_->kv_heads(), attention_->head_dim(),
+                    cache_dtype(*this) == DType::bf16, L, cache.length() + L, splits, chunk);
     decode_layer(*this, x.data<float>(), static_cast<float*>(mutable_data(out)), B, L, cache, ws, splits, chunk, context);
     return out;
 }
@@ -366,7 +367,9 @@ Tensor TransformerDecoder::decode(const Tensor& input, std::span<KVCache> cache)
         float* xd = static_cast<float*>(mutable_data(x));
         DecodeWorkspace ws;
         int splits = 1, chunk = 64;
-        attention_split(B, layers_.front()->attention().kv_heads(), L, prefix + L, splits, chunk);
+        const auto& front = layers_.front()->attention();
+        attention_split(B, front.heads(), front.kv_heads(), front.head_dim(),
+                        cache_dtype(*layers_.front()) == DType::bf16, L, prefix + L, splits, chunk);
         for (std::size_t i = 0; i < layers_.size(); ++i) {
             cache[i].reserve(B, layers_[i]->attention().kv_heads(), layers_[i]->attention().head_dim(),
                              cache_dtype(*layers_[i]), input.device());

@@ -79,7 +79,8 @@ void DecoderLM::forward_chunk(const Index* ids, Index batch, Index length, std::
     const auto& first = decoder_->layer(0).attention();
     int splits = 1, chunk = 64;
     const Index source = capacity_splits ? cache.front().capacity() : cache.front().length() + length;
-    attention_split(batch, first.kv_heads(), length, source, splits, chunk);
+    attention_split(batch, first.heads(), first.kv_heads(), first.head_dim(),
+                    cache_dtype(decoder_->layer(0)) == DType::bf16, length, source, splits, chunk);
     for (Index i = 0; i < decoder_->layer_count(); ++i) {
         auto& layer = decoder_->layer(i);
         cache[static_cast<std::size_t>(i)].reserve(batch, layer.attention().kv_heads(), layer.attention().head_dim(),

@@ -78,12 +78,19 @@ void linear_into(const float* x, Index rows, Index k, const Tensor& weight, cons
     hip_check(dlk_gemv(&p, context.stream), "linear");
 }
 
-void attention_split(Index batch, Index kv_heads, Index length, Index source, int& splits, int& chunk) {
+void attention_split(Index batch, Index heads, Index kv_heads, Index head_dim, bool kv_bf16, Index length,
+                     Index source, int& splits, int& chunk) {
     constexpr Index tile = 64;
     if (length == 1) {
-        // one new position: splits of DLK_DECODE_CHUNK keys, one 64-key tile per wave of a work-group
-        splits = static_cast<int>(std::max<Index>(1, (source + DLK_DECODE_CHUNK - 1) / DLK_DECODE_CHUNK));
-        chunk = DLK_DECODE_CHUNK;
+        // one new position: one 64-key tile per wave, 4..16 waves per work-group merging in LDS; split only
+        // beyond the widest work-group (the split partials take a second, combine launch)
+        Index widest = dlk_attention_decode_chunk(static_cast<int>(heads), static_cast<int>(kv_heads),
+                                                  static_cast<int>(head_dim), kv_bf16 ? 1 : 0);
+        if (widest <= 0) widest = DLK_DECODE_CHUNK_MAX; // the general kernel takes any multiple of its tile
+        Index per = 4 * tile;
+        while (per < source && per < widest) per *= 2;
+        chunk = static_cast<int>(per);
+        splits = static_cast<int>(std::max<Index>(1, (source + per - 1) / per));
         return;
     }
     const Index groups = batch * kv_heads;
@@ -211,7 +218,7 @@ Tensor grouped_query_attention(const Tensor& query, const Tensor& key, const Ten
     p.out = static_cast<float*>(mutable_data(out));
     p.ldo = H * D;
     if (S < L) throw std::invalid_argument("grouped_query_attention: needs S >= L");
-    attention_split(B, KV, L, S, p.splits, p.chunk);
+    attention_split(B, H, KV, D, kv_dtype == DType::bf16, L, S, p.splits, p.chunk);
     Tensor po, pml;
     if (p.splits > 1) {
         po = empty_tensor({B * H * L, p.splits, D}, DType::f32, query.device());

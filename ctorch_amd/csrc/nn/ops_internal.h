@@ -20,7 +20,8 @@ dlk_gemv_params gemv_params(const float* x, Index rows, Index k, int epilogue);
 void linear_into(const float* x, Index rows, Index k, const Tensor& weight, const std::optional<Tensor>& bias,
                  float* y, Index ldy, GpuContext& context);
 
-/// Number of key splits and keys per split for decode attention over `source` keys.
-void attention_split(Index batch, Index kv_heads, Index length, Index source, int& splits, int& chunk);
+/// Number of key splits and keys per split for attention of `length` new positions over `source` keys.
+void attention_split(Index batch, Index heads, Index kv_heads, Index head_dim, bool kv_bf16, Index length,
+                     Index source, int& splits, int& chunk);
 
 } // namespace dl::detail

@@ -153,8 +153,10 @@ def test_operators_match_the_oracle():
         vv = rng.standard_normal((2, 2, S, 64)).astype(np.float32)
         y = ct.grouped_query_attention(G(qq), G(kk), G(vv)).numpy()
         assert np.max(np.abs(y - oracle.attention(qq, kk, vv, -1))) <= 1e-5
-    # one position over bf16 K/V: the decode kernel, with 1..3 key chunks of 256 merged by the combine pass
-    for S, hd, heads in ((1, 64, 8), (64, 64, 8), (200, 64, 8), (257, 64, 8), (700, 64, 16), (300, 128, 8)):
+    # one position over bf16 K/V: the decode kernel (4..16 waves of 64 keys per work-group); past the widest
+    # work-group the keys split and the combine launch merges the partials
+    for S, hd, heads in ((1, 64, 8), (64, 64, 8), (200, 64, 8), (257, 64, 8), (700, 64, 16), (300, 128, 8),
+                         (1500, 64, 8), (1100, 64, 2)):
         qq = rng.standard_normal((2, heads, 1, hd)).astype(np.float32)
         kb = oracle.bf16_encode(rng.standard_normal((2, 2, S, hd)).astype(np.float32))
         vb = oracle.bf16_encode(rng.standard_normal((2, 2, S, hd)).astype(np.float32))
@@ -186,8 +188,8 @@ def test_batched_decode_over_a_seeded_prefix():
         ids = want.argmax(-1).reshape(B, 1)
 
 
-def test_decode_across_key_chunks_merges_in_kernel():
-    say("case: B=2 decode over a 600-token prefix, head dim 64, 4 query heads per KV head (3 key chunks)")
+def test_decode_over_split_keys_merges_partials():
+    say("case: B=2 decode over a 600-token prefix, head dim 64, 4 query heads per KV head (2 key splits)")
     cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=512, context=640,
                              dtype="bf16")
     ref, gpu = build_pair(cfg, root=(43, 0), scale=0.05)
@@ -200,7 +202,7 @@ def test_decode_across_key_chunks_merges_in_kernel():
         gc.append(layer, ct.Tensor.from_numpy(kb, ct.BF16, GPU), ct.Tensor.from_numpy(vb, ct.BF16, GPU))
         rc.fill(layer, P, oracle.bf16_decode(kb), oracle.bf16_decode(vb))
     ids = oracle.random_ids((80, 0), B, cfg.vocab).reshape(B, 1)
-    for step in range(3):  # eager steps: split count from the live length, merged by the last chunk to finish
+    for step in range(3):  # eager steps: split count from the live length, partials merged by the combine launch
         want = ref.logits(ids, rc)[:, -1]
         got = gpu.logits(ids, gc)
         assert np.max(np.abs(got - want)) <= 2e-2, step
