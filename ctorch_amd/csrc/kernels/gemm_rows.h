@@ -1,0 +1,522 @@
+// Projection over several activation rows (batched decode, M = 3..64 per launch) on the matrix cores, with the
+// epilogues of the GEMV (see dlk_gemv_params in kernels.h).
+//
+// One v_mfma_f32_16x16x32_bf16 computes D[16 weight rows][16 activation rows] += W[16][32] * X[16][32]^T.  Lane
+// l supplies A = W[row l%16][k 8*(l/16) .. +8] (16 contiguous bytes of a weight row, so the weights stream from
+// HBM in their row-major layout), B = X[row l%16][k 8*(l/16) .. +8], and receives D[rows 4*(l/16) .. +4][l%16].
+//
+// A work-group is four waves; each wave owns one tile of 16 weight rows and all activation rows (MT tiles of
+// 16).  The activation rows are staged per K-chunk in LDS as bf16 pairs hi + lo (x = hi + lo to ~2^-16), so every
+// product is two MFMAs and the result keeps f32-level accuracy against a bf16 weight.  The RMSNorm of the
+// activation rows is fused: the staged rows are x * g, the sums of squares accumulate while staging, and the
+// per-row factor 1/sqrt(mean x^2 + eps) scales the finished dot products.  Chunks are double buffered in LDS;
+// the next chunk's activations (into registers) and weights are loaded while the current chunk is used.
+//
+// Tile rows: generic epilogues take 16 consecutive rows of one weight segment; SwiGLU interleaves gate and up
+// (tile row 2j = gate row 8T + j, 2j + 1 = up row 8T + j), so every lane holds (gate, up) pairs and QKV holds
+// RoPE pairs (rows 2j, 2j + 1 of a head) in one lane.
+#pragma once
+
+#include "kernels/gemv_impl.h"
+
+namespace dlk::gemm {
+
+using gemv::u32x4;
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kTile = 16;                       // weight rows per wave tile
+constexpr int kMaxRows = 64;                    // activation rows per launch
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+/// k per staged chunk: the double-buffered hi/lo rows stay within 64 KB of LDS.
+constexpr int chunk_k(int mt) { return mt == 1 ? 256 : mt == 2 ? 128 : 64; }
+constexpr int lds_stride(int mt) { return chunk_k(mt) + 8; } // bf16 elements per staged row (bank spread)
+constexpr size_t lds_bytes(int mt) { return size_t(2) * 2 * 16 * mt * lds_stride(mt) * 2; }
+
+/// Whether the matrix-core path takes these parameters (host side).
+inline bool eligible(const dlk_gemv_params& p) {
+    if (!p.w_bf16 || p.M < 3 || p.K % 256 != 0 || p.K < 512) return false;
+    if (p.epilogue == DLK_EPI_SWIGLU) return p.seg_rows[0] % 8 == 0;
+    for (int s = 0; s < p.nseg; ++s)
+        if (p.seg_rows[s] % kTile != 0) return false;
+    return true;
+}
+
+/// 16-row weight tiles of a launch.
+__host__ __device__ inline int tiles_of(const dlk_gemv_params& p) {
+    if (p.epilogue == DLK_EPI_SWIGLU) return p.seg_rows[0] / 8;
+    int t = p.seg_rows[0] / kTile;
+    if (p.nseg > 1) t += p.seg_rows[1] / kTile;
+    if (p.nseg > 2) t += p.seg_rows[2] / kTile;
+    return t;
+}
+
+inline int blocks_of(const dlk_gemv_params& p) { return (tiles_of(p) + kWaves - 1) / kWaves; }
+
+/// Activation tiles of 16 rows for a launch of `rows` (<= 64) rows.
+inline int row_tiles(int rows) { return rows <= 16 ? 1 : rows <= 32 ? 2 : 4; }
+
+/// Key slices of a launch: one, unless the weight tiles leave most CUs idle; then the fewest slices (each a
+/// whole number of chunks, at least two) that give 256 work-groups, or the most that divide the chunks.
+inline int splits_of(const dlk_gemv_params& p, int rows) {
+    if (p.epilogue == DLK_EPI_LOGITS) return 1;
+    const int blocks = blocks_of(p);
+    if (blocks >= 192) return 1;
+    const int chunks = p.K / chunk_k(row_tiles(rows));
+    int best = 1;
+    for (int s = 2; s <= 16; ++s) {
+        if (chunks % s != 0 || chunks / s < 2) continue;
+        best = s;
+        if (blocks * s >= 256) break;
+    }
+    return best;
+}
+
+/// Workspace floats of a split launch of `rows` rows: partial dots [S][rows][tiles * 16], then squares [S][rows].
+inline int64_t split_floats(const dlk_gemv_params& p, int splits, int rows) {
+    return splits <= 1 ? 0 : static_cast<int64_t>(splits) * rows * (tiles_of(p) * kTile + 1);
+}
+
+// A wave's tile: segment, first row in the segment, the matrix of tile row i.
+struct TileMap {
+    int seg, n0, rows;
+    const uint16_t *base0, *base1;
+};
+
+template <bool SWIGLU>
+__device__ __forceinline__ TileMap locate(const dlk_gemv_params& p, int tile) {
+    const uint16_t* w0 = static_cast<const uint16_t*>(p.w[0]);
+    const uint16_t* w1 = static_cast<const uint16_t*>(p.w[1]);
+    const uint16_t* w2 = static_cast<const uint16_t*>(p.w[2]);
+    if constexpr (SWIGLU) return {0, tile * 8, p.seg_rows[0], w0, w1};
+    const int t0 = p.seg_rows[0] / kTile, t1 = p.nseg > 1 ? p.seg_rows[1] / kTile : 0;
+    if (tile < t0 || p.nseg == 1) return {0, tile * kTile, p.seg_rows[0], w0, w0};
+    if (tile < t0 + t1 || p.nseg == 2) return {1, (tile - t0) * kTile, p.seg_rows[1], w1, w1};
+    return {2, (tile - t0 - t1) * kTile, p.seg_rows[2], w2, w2};
+}
+
+// weight row of tile row i (SwiGLU: even rows gate, odd rows up of the same output)
+template <bool SWIGLU>
+__device__ __forceinline__ const uint16_t* tile_row(const TileMap& t, int i, int K) {
+    if constexpr (SWIGLU) return (i & 1 ? t.base1 : t.base0) + static_cast<int64_t>(t.n0 + i / 2) * K;
+    return t.base0 + static_cast<int64_t>(t.n0 + i) * K;
+}
+
+__device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
+    hi = f32_to_bf16(v);
+    lo = f32_to_bf16(v - bf16_to_f32(hi));
+}
+
+// The epilogue of one lane: v[j] = finished dot products of tile rows 4q + j (q = lane / 16) for activation
+// row m of the launch.
+template <int EPI>
+__device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const TileMap& t, int q, int m,
+                                              const float (&v)[4], double& best_score, int64_t& best_index,
+                                              uint64_t seed, uint64_t stream) {
+    using Traits = gemv::WeightTraits<uint16_t>;
+    if constexpr (EPI == DLK_EPI_SWIGLU) {
+        const int n = t.n0 + 2 * q;
+        p.y[static_cast<int64_t>(m) * p.ldy + n] = gemv::silu(v[0]) * v[1];
+        p.y[static_cast<int64_t>(m) * p.ldy + n + 1] = gemv::silu(v[2]) * v[3];
+    } else if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = t.n0 + 4 * q + j;
+            float out = v[j];
+            if constexpr (EPI == DLK_EPI_STORE) {
+                if (p.bias)
+                    out += p.bias_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.bias)[n])
+                                       : static_cast<const float*>(p.bias)[n];
+            } else {
+                out += p.residual[static_cast<int64_t>(m) * p.ldres + n];
+            }
+            p.y[static_cast<int64_t>(m) * p.ldy + n] = out;
+        }
+    } else if constexpr (EPI == DLK_EPI_QKV) {
+        const int64_t mg = p.m_base + m;
+        const int64_t b = mg / p.length, pos = *p.position + mg % p.length;
+        const int hd = p.head_dim;
+        const float* hidden = t.seg == 0 ? p.lora_hidden[0] : t.seg == 2 ? p.lora_hidden[2] : nullptr;
+        const void* lora_up = t.seg == 0 ? p.lora_up[0] : p.lora_up[2];
+#pragma unroll
+        for (int pair = 0; pair < 2; ++pair) {
+            const int n = t.n0 + 4 * q + 2 * pair; // even: the pair (n, n + 1) shares one rotation
+            float even = v[2 * pair], odd = v[2 * pair + 1];
+            if (hidden) {
+                // unmerged LoRA: + scale * up[n, :] . hidden[m, :]
+                const float* hrow = hidden + mg * p.lora_rank;
+                float de = 0.0f, dodd = 0.0f;
+                for (int j = 0; j < p.lora_rank; ++j) {
+                    de += Traits::scalar(lora_up, static_cast<int64_t>(n) * p.lora_rank + j) * hrow[j];
+                    dodd += Traits::scalar(lora_up, static_cast<int64_t>(n + 1) * p.lora_rank + j) * hrow[j];
+                }
+                even += de * p.lora_scale;
+                odd += dodd * p.lora_scale;
+            }
+            const int d = n % hd, head = n / hd;
+            if (t.seg < 2) {
+                // even: x_e c - x_o s ; odd: x_e s + x_o c (interleaved pairs, src/ops/contraction.cpp:44-49)
+                const int64_t table = pos * (hd / 2) + d / 2;
+                const float c = p.cosine[table], s = p.sine[table];
+                const float re = even * c - odd * s, ro = even * s + odd * c;
+                even = re;
+                odd = ro;
+            }
+            if (t.seg == 0) {
+                p.y[mg * p.ldy + n] = even;
+                p.y[mg * p.ldy + n + 1] = odd;
+            } else {
+                const int64_t index = ((b * p.kv_heads + head) * p.cache_capacity + pos) * hd + d;
+                void* cache = t.seg == 1 ? p.k_cache : p.v_cache;
+                if (p.cache_bf16) {
+                    static_cast<uint16_t*>(cache)[index] = f32_to_bf16(even);
+                    static_cast<uint16_t*>(cache)[index + 1] = f32_to_bf16(odd);
+                } else {
+                    static_cast<float*>(cache)[index] = even;
+                    static_cast<float*>(cache)[index + 1] = odd;
+                }
+            }
+        }
+    } else if constexpr (EPI == DLK_EPI_LOGITS) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = t.n0 + 4 * q + j;
+            if (p.y) p.y[static_cast<int64_t>(m) * p.ldy + n] = v[j];
+            if (p.sample_mode != 0) {
+                const int64_t mg = p.m_base + m;
+                const double s = sample_score(v[j], p.sample_mode, p.temperature, seed, stream,
+                                              static_cast<uint64_t>(mg * t.rows + n));
+                if (best_index < 0 || prefer(s, n, best_score, best_index)) {
+                    best_score = s;
+                    best_index = n;
+                }
+            }
+        }
+    }
+}
+
+template <int EPI, bool NORM, int MT>
+__global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
+    constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
+    constexpr int RM = 16 * MT;            // staged activation rows
+    constexpr int KC = chunk_k(MT);        // k per chunk
+    constexpr int STRIDE = lds_stride(MT); // bf16 per staged row
+    constexpr int STEPS = KC / 32;         // MFMA k-steps per chunk
+    constexpr int COLS = KC / 4;           // staging: lanes per row (4 columns each)
+    constexpr int ROWS_PER_PASS = kThreads / COLS;
+    constexpr int XR = RM / ROWS_PER_PASS; // staging loads per thread per chunk
+    static_assert(RM % ROWS_PER_PASS == 0, "staging covers the rows");
+    extern __shared__ uint16_t lds[];      // [2 buffers][hi, lo][RM][STRIDE]
+    __shared__ float row_squares[RM];
+    __shared__ double pool_score[kWaves][RM];
+    __shared__ int64_t pool_index[kWaves][RM];
+
+    const int t = threadIdx.x, lane = t % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int K = p.K, splits = gridDim.y, slice = K / splits, k_begin = blockIdx.y * slice;
+    const int nchunks = slice / KC;
+    const int tiles = tiles_of(p);
+    const int my_tile = blockIdx.x * kWaves + wave;
+    const bool active = my_tile < tiles;
+    // idle waves of the last work-group stream a valid tile (unused) so no load sits in a branch
+    const TileMap tm = locate<SWIGLU>(p, min(my_tile, tiles - 1));
+    const uint16_t* wrow = tile_row<SWIGLU>(tm, lane % 16, K) + k_begin + 8 * (lane / 16);
+
+    // staging: thread -> (column group c4, rows r0, r0 + ROWS_PER_PASS, ...)
+    const int c4 = t % COLS, r0 = t / COLS;
+    const bool norm = NORM && p.apply_norm;
+    const bool affine = norm && p.norm_weight;
+    const int esize = p.norm_bf16 ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t gres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(affine ? p.norm_weight : static_cast<const void*>(p.x)), 0, affine ? K * esize : 0,
+        kBufferFlags);
+
+    float4 xr[XR];
+    u32x4 graw;
+    auto load_x = [&](int c) {
+        const int k = k_begin + c * KC + 4 * c4;
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            const int m = min(r0 + i * ROWS_PER_PASS, p.M - 1);
+            xr[i] = *reinterpret_cast<const float4*>(p.x + static_cast<int64_t>(m) * p.ldx + k);
+        }
+        if constexpr (NORM) graw = __builtin_amdgcn_raw_buffer_load_b128(gres, k * esize, 0, 0);
+    };
+    float squares[XR];
+#pragma unroll
+    for (int i = 0; i < XR; ++i) squares[i] = 0.0f;
+    auto stage = [&](int buf) {
+        float g[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        if constexpr (NORM) {
+            if (affine) {
+                if (p.norm_bf16) {
+                    g[0] = bf16_lo(graw.x); g[1] = bf16_hi(graw.x); g[2] = bf16_lo(graw.y); g[3] = bf16_hi(graw.y);
+                } else {
+                    g[0] = __uint_as_float(graw.x); g[1] = __uint_as_float(graw.y);
+                    g[2] = __uint_as_float(graw.z); g[3] = __uint_as_float(graw.w);
+                }
+            }
+        }
+        uint16_t* hi = lds + buf * 2 * RM * STRIDE;
+        uint16_t* lo = hi + RM * STRIDE;
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            const int m = r0 + i * ROWS_PER_PASS;
+            float4 v = xr[i];
+            if (m >= p.M) v = make_float4(0.f, 0.f, 0.f, 0.f);
+            squares[i] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            const float e[4] = {v.x * g[0], v.y * g[1], v.z * g[2], v.w * g[3]};
+            uint16_t h[4], l[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) split_bf16(e[j], h[j], l[j]);
+            *reinterpret_cast<uint2*>(hi + m * STRIDE + 4 * c4) =
+                make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+            *reinterpret_cast<uint2*>(lo + m * STRIDE + 4 * c4) =
+                make_uint2(l[0] | (static_cast<uint32_t>(l[1]) << 16), l[2] | (static_cast<uint32_t>(l[3]) << 16));
+        }
+    };
+    u32x4 wa[STEPS], wb[STEPS];
+    auto load_w = [&](int c, u32x4 (&dst)[STEPS]) {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s)
+            dst[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + c * KC + 32 * s));
+    };
+    f32x4 acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int buf, const u32x4 (&w)[STEPS]) {
+        const uint16_t* hi = lds + buf * 2 * RM * STRIDE;
+        const uint16_t* lo = hi + RM * STRIDE;
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const bf16x8 a = __builtin_bit_cast(bf16x8, w[s]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int off = (16 * mt + lane % 16) * STRIDE + 32 * s + 8 * (lane / 16);
+                const bf16x8 bh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(hi + off));
+                const bf16x8 bl = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lo + off));
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh, acc[mt], 0, 0, 0);
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl, acc[mt], 0, 0, 0);
+            }
+        }
+    };
+
+    // Invariant at the top of each pair of chunks (c, c + 1): LDS buffer 0 holds chunk c, the registers hold
+    // chunk c + 1's activations, and the weights of c (wa) and c + 1 (wb) are loaded or in flight.  Loads in
+    // the loop are unconditional (a load on one path of a branch would drain every load at the next wait); the
+    // last two or three chunks are peeled.  nchunks >= 2 (the host requires K >= 2 * chunk).
+    load_x(0);
+    load_w(0, wa);
+    stage(0);
+    load_x(1);
+    load_w(1, wb);
+    gemv::lds_barrier();
+    int c = 0;
+    for (; c + 3 < nchunks; c += 2) {
+        compute(0, wa);
+        stage(1);
+        load_x(c + 2);
+        load_w(c + 2, wa);
+        gemv::lds_barrier();
+        compute(1, wb);
+        stage(0);
+        load_x(c + 3);
+        load_w(c + 3, wb);
+        gemv::lds_barrier();
+    }
+    compute(0, wa); // chunk c
+    stage(1);       // chunk c + 1
+    if (c + 2 < nchunks) {
+        load_x(c + 2);
+        load_w(c + 2, wa);
+    }
+    gemv::lds_barrier();
+    compute(1, wb); // chunk c + 1
+    if (c + 2 < nchunks) {
+        stage(0);
+        gemv::lds_barrier();
+        compute(0, wa); // chunk c + 2
+    }
+
+    // per-row norm factor: every row belongs to one staging pass row, summed across the lanes that staged it
+    if (norm) {
+#pragma unroll
+        for (int i = 0; i < XR; ++i) {
+            // lanes t with the same r0 staged disjoint columns of row r0 + i * ROWS_PER_PASS
+            float s = squares[i];
+            if constexpr (COLS == kWave) {
+                s = wave_sum(s);
+                if (lane == 0) row_squares[r0 + i * ROWS_PER_PASS] = s;
+            } else {
+                // COLS = 32 or 16 lanes per row: reduce within the row's lane group
+#pragma unroll
+                for (int off = COLS / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
+                if (c4 == 0) row_squares[r0 + i * ROWS_PER_PASS] = s;
+            }
+        }
+    }
+    gemv::lds_barrier();
+
+    const int q = lane / 16;
+    if (splits > 1) {
+        // key slice: raw partial dots and this slice's row sums of squares; gemm_reduce finishes them
+        const int64_t width = static_cast<int64_t>(tiles) * kTile;
+        float* part = p.split_partial + static_cast<int64_t>(blockIdx.y) * p.M * width;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int m = 16 * mt + lane % 16;
+            if (active && m < p.M)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) part[m * width + my_tile * kTile + 4 * q + j] = acc[mt][j];
+        }
+        if (norm && blockIdx.x == 0 && t < p.M)
+            p.split_partial[static_cast<int64_t>(splits) * p.M * width + blockIdx.y * p.M + t] = row_squares[t];
+        return;
+    }
+
+    // epilogue: lane holds D[4q + j][m] of each activation tile
+    double best_score = 0.0;
+    int64_t best_index = -1;
+    uint64_t seed = p.key_seed, stream = p.key_stream;
+    if constexpr (EPI == DLK_EPI_LOGITS) {
+        if (p.sample_mode == 2 && p.key_label)
+            fold_in(p.key_seed, p.key_stream, static_cast<uint64_t>(*p.key_label), seed, stream);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + lane % 16;
+        double bs = 0.0;
+        int64_t bi = -1;
+        if (active && m < p.M) {
+            const float inv = norm ? rsqrtf(row_squares[m] / static_cast<float>(K) + p.epsilon) : 1.0f;
+            const float v[4] = {acc[mt][0] * inv * p.acc_scale, acc[mt][1] * inv * p.acc_scale,
+                                acc[mt][2] * inv * p.acc_scale, acc[mt][3] * inv * p.acc_scale};
+            lane_epilogue<EPI>(p, tm, q, m, v, bs, bi, seed, stream);
+        }
+        if constexpr (EPI == DLK_EPI_LOGITS) {
+            // the 4 lanes of row m (q = 0..3) -> one candidate; then the 4 waves through LDS
+#pragma unroll
+            for (int off = 16; off < kWave; off <<= 1) {
+                const double os = __shfl_xor(bs, off, kWave);
+                const int64_t oi = __shfl_xor(bi, off, kWave);
+                if (oi >= 0 && (bi < 0 || prefer(os, oi, bs, bi))) {
+                    bs = os;
+                    bi = oi;
+                }
+            }
+            if (q == 0) {
+                pool_score[wave][m] = bs;
+                pool_index[wave][m] = bi;
+            }
+        }
+    }
+    if constexpr (EPI == DLK_EPI_LOGITS) {
+        if (p.sample_mode != 0) {
+            gemv::lds_barrier();
+            if (wave == 0) {
+                for (int m = lane; m < RM && m < p.M; m += kWave) {
+                    double bs = 0.0;
+                    int64_t bi = -1;
+#pragma unroll
+                    for (int w = 0; w < kWaves; ++w) {
+                        const int64_t j = pool_index[w][m];
+                        if (j >= 0 && (bi < 0 || prefer(pool_score[w][m], j, bs, bi))) {
+                            bs = pool_score[w][m];
+                            bi = j;
+                        }
+                    }
+                    dlk_sample_partial out;
+                    out.score = bs;
+                    out.index = bi;
+                    p.partial[(p.m_base + m) * p.partial_blocks + blockIdx.x] = out;
+                }
+            }
+        }
+    }
+    if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL) {
+        if (p.bump_position && blockIdx.x == 0 && t == 0) *p.bump_position += p.bump_count;
+    }
+}
+
+// Second launch of a key-split projection: thread (m, tile, q) sums the S partial dots of tile rows 4q .. 4q+3
+// for activation row m in slice order, applies the row's norm factor, and runs the lane epilogue.
+template <int EPI, bool NORM>
+__global__ __launch_bounds__(kThreads) void gemm_reduce(const dlk_gemv_params p, int splits) {
+    constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
+    const int tiles = tiles_of(p);
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const int q = static_cast<int>(idx % 4);
+    const int tile = static_cast<int>((idx / 4) % tiles);
+    const int m = static_cast<int>(idx / (4 * static_cast<int64_t>(tiles)));
+    if (m < p.M) {
+        const int64_t width = static_cast<int64_t>(tiles) * kTile;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        float squares = 0.0f;
+        for (int s = 0; s < splits; ++s) {
+            const float* part = p.split_partial + (static_cast<int64_t>(s) * p.M + m) * width + tile * kTile + 4 * q;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] += part[j];
+            if constexpr (NORM) squares += p.split_partial[static_cast<int64_t>(splits) * p.M * width + s * p.M + m];
+        }
+        const float inv = NORM && p.apply_norm ? rsqrtf(squares / static_cast<float>(p.K) + p.epsilon) : 1.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] *= inv * p.acc_scale;
+        double bs = 0.0;
+        int64_t bi = -1;
+        lane_epilogue<EPI>(p, locate<SWIGLU>(p, tile), q, m, v, bs, bi, p.key_seed, p.key_stream);
+    }
+    if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL) {
+        if (p.bump_position && blockIdx.x == 0 && threadIdx.x == 0) *p.bump_position += p.bump_count;
+    }
+}
+
+/// The reduce kernel of a key-split launch; {} if none.
+template <int EPI>
+gemv::Kernel resolve_reduce(const dlk_gemv_params& p) {
+    if constexpr (EPI == DLK_EPI_LOGITS) {
+        return {};
+    } else {
+        if (gemv::norm_variant(EPI, p.apply_norm != 0)) {
+            if constexpr (EPI != DLK_EPI_RESIDUAL)
+                return {reinterpret_cast<const void*>(&gemm_reduce<EPI, true>), 0};
+            return {};
+        }
+        if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL)
+            return {reinterpret_cast<const void*>(&gemm_reduce<EPI, false>), 0};
+        return {};
+    }
+}
+
+/// The matrix-core kernel for mt (1, 2 or 4) activation tiles; {} if none.
+template <int EPI>
+gemv::Kernel resolve(const dlk_gemv_params& p, int mt) {
+    auto pick = [&](auto norm) -> gemv::Kernel {
+        constexpr bool N = decltype(norm)::value;
+        switch (mt) {
+        case 1: return {reinterpret_cast<const void*>(&gemm_rows<EPI, N, 1>), lds_bytes(1)};
+        case 2: return {reinterpret_cast<const void*>(&gemm_rows<EPI, N, 2>), lds_bytes(2)};
+        case 4: return {reinterpret_cast<const void*>(&gemm_rows<EPI, N, 4>), lds_bytes(4)};
+        default: return {};
+        }
+    };
+    if (gemv::norm_variant(EPI, p.apply_norm != 0)) {
+        if constexpr (EPI != DLK_EPI_RESIDUAL) return pick(std::true_type{});
+        return {};
+    }
+    if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL) return pick(std::false_type{});
+    return {};
+}
+
+} // namespace dlk::gemm
+
+dlk::gemv::Kernel dlk_gemm_kernel_store(const dlk_gemv_params& p, int mt);
+dlk::gemv::Kernel dlk_gemm_kernel_residual(const dlk_gemv_params& p, int mt);
+dlk::gemv::Kernel dlk_gemm_kernel_qkv(const dlk_gemv_params& p, int mt);
+dlk::gemv::Kernel dlk_gemm_kernel_swiglu(const dlk_gemv_params& p, int mt);
+dlk::gemv::Kernel dlk_gemm_kernel_logits(const dlk_gemv_params& p, int mt);
+dlk::gemv::Kernel dlk_gemm_reduce_store(const dlk_gemv_params& p);
+dlk::gemv::Kernel dlk_gemm_reduce_residual(const dlk_gemv_params& p);
+dlk::gemv::Kernel dlk_gemm_reduce_qkv(const dlk_gemv_params& p);
+dlk::gemv::Kernel dlk_gemm_reduce_swiglu(const dlk_gemv_params& p);
+dlk::gemv::Kernel dlk_gemm_reduce_logits(const dlk_gemv_params& p);

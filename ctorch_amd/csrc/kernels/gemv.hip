@@ -1,9 +1,10 @@
-// Host dispatch of the projection GEMV (kernels in gemv_impl.h, instantiated per epilogue in gemv_*.hip).
+// Host dispatch of the projections: the GEMV (gemv_impl.h) for one or two activation rows (or shapes the matrix
+// cores do not take), the matrix-core kernel (gemm_rows.h) for more; both instantiated per epilogue in gemv_*.hip.
 //
 // The grid is persistent: one wave per row group, capped at the number of waves the chosen kernel keeps
 // resident on the device (its occupancy times the CU count), so every wave streams from the start and none
 // waits for another to retire.  LOGITS launches write one sampling candidate per work-group.
-#include "kernels/gemv_impl.h"
+#include "kernels/gemm_rows.h"
 
 #include <mutex>
 #include <unordered_map>
@@ -24,6 +25,65 @@ Kernel resolve(const dlk_gemv_params& p, int mt) {
 }
 
 int activation_tile(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : 4; }
+
+Kernel resolve_gemm(const dlk_gemv_params& p, int mt) {
+    switch (p.epilogue) {
+    case DLK_EPI_STORE: return dlk_gemm_kernel_store(p, mt);
+    case DLK_EPI_RESIDUAL: return dlk_gemm_kernel_residual(p, mt);
+    case DLK_EPI_QKV: return dlk_gemm_kernel_qkv(p, mt);
+    case DLK_EPI_SWIGLU: return dlk_gemm_kernel_swiglu(p, mt);
+    case DLK_EPI_LOGITS: return dlk_gemm_kernel_logits(p, mt);
+    default: return {};
+    }
+}
+
+Kernel resolve_reduce(const dlk_gemv_params& p) {
+    switch (p.epilogue) {
+    case DLK_EPI_STORE: return dlk_gemm_reduce_store(p);
+    case DLK_EPI_RESIDUAL: return dlk_gemm_reduce_residual(p);
+    case DLK_EPI_QKV: return dlk_gemm_reduce_qkv(p);
+    case DLK_EPI_SWIGLU: return dlk_gemm_reduce_swiglu(p);
+    case DLK_EPI_LOGITS: return dlk_gemm_reduce_logits(p);
+    default: return {};
+    }
+}
+
+int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
+    using namespace dlk::gemm;
+    const int blocks = blocks_of(params);
+    if (params.epilogue == DLK_EPI_LOGITS && params.sample_mode != 0 && params.partial_blocks != blocks)
+        return static_cast<int>(hipErrorInvalidValue);
+    dlk_gemv_params p = params;
+    for (int m0 = 0; m0 < params.M; m0 += kMaxRows) {
+        p.M = std::min(kMaxRows, params.M - m0);
+        p.x = params.x + static_cast<int64_t>(m0) * params.ldx;
+        p.m_base = params.m_base + m0;
+        if (params.epilogue != DLK_EPI_QKV) p.y = params.y ? params.y + static_cast<int64_t>(m0) * params.ldy : nullptr;
+        if (params.residual) p.residual = params.residual + static_cast<int64_t>(m0) * params.ldres;
+        p.bump_position = m0 + kMaxRows >= params.M ? params.bump_position : nullptr;
+        const Kernel kernel = resolve_gemm(p, row_tiles(p.M));
+        if (!kernel.fn) return static_cast<int>(hipErrorInvalidValue);
+        // key slices when the tiles leave CUs idle and the caller gave room for the partials
+        int splits = splits_of(p, p.M);
+        if (splits > 1 && (!p.split_partial || p.split_capacity < split_floats(p, splits, p.M))) splits = 1;
+        const int64_t* bump = p.bump_position;
+        if (splits > 1) p.bump_position = nullptr; // the reduce launch advances the length
+        void* args[] = {&p};
+        hipError_t status = hipLaunchKernel(kernel.fn, dim3(blocks, splits), dim3(kThreads), args, kernel.lds, stream);
+        if (status != hipSuccess) return static_cast<int>(status);
+        if (splits > 1) {
+            p.bump_position = const_cast<int64_t*>(bump);
+            const Kernel reduce = resolve_reduce(p);
+            if (!reduce.fn) return static_cast<int>(hipErrorInvalidValue);
+            const int64_t threads = static_cast<int64_t>(p.M) * tiles_of(p) * 4;
+            void* rargs[] = {&p, &splits};
+            status = hipLaunchKernel(reduce.fn, dim3(static_cast<unsigned>((threads + kThreads - 1) / kThreads)),
+                                     dim3(kThreads), rargs, 0, stream);
+            if (status != hipSuccess) return static_cast<int>(status);
+        }
+    }
+    return 0;
+}
 
 // resident waves of a kernel on the current device (0 on error)
 int resident_waves(const Kernel& kernel) {
@@ -62,8 +122,15 @@ int launch_waves(const dlk_gemv_params& p) {
 
 } // namespace
 
+extern "C" int64_t dlk_gemv_split_floats(const dlk_gemv_params* p) {
+    if (!dlk::gemm::eligible(*p)) return 0;
+    const int rows = std::min(p->M, dlk::gemm::kMaxRows);
+    return dlk::gemm::split_floats(*p, dlk::gemm::splits_of(*p, rows), rows);
+}
+
 extern "C" int dlk_gemv_blocks(const dlk_gemv_params* p) {
     // LOGITS: one sampling candidate per work-group of the launch
+    if (dlk::gemm::eligible(*p)) return dlk::gemm::blocks_of(*p);
     const int waves = launch_waves(*p);
     return waves > 0 ? (waves + dlk::gemv::kWavesPerBlock - 1) / dlk::gemv::kWavesPerBlock : -1;
 }
@@ -82,6 +149,7 @@ extern "C" int dlk_gemv(const dlk_gemv_params* params, dlh_stream stream_handle)
     if (params->epilogue == DLK_EPI_QKV)
         for (int s = 0; s < params->nseg; ++s)
             if (params->seg_rows[s] % 2 != 0 || params->head_dim % 2 != 0) return static_cast<int>(hipErrorInvalidValue);
+    if (dlk::gemm::eligible(*params)) return launch_gemm(*params, stream);
     const int waves = launch_waves(*params);
     if (waves <= 0) return static_cast<int>(hipErrorInvalidValue);
     const int blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;

@@ -1,6 +1,14 @@
-// Projection GEMV kernels with the SWIGLU epilogue.
-#include "kernels/gemv_impl.h"
+// Projection kernels with the SWIGLU epilogue: the GEMV (one activation row) and the matrix-core variant.
+#include "kernels/gemm_rows.h"
 
 dlk::gemv::Kernel dlk_gemv_kernel_swiglu(const dlk_gemv_params& p, int mt) {
     return dlk::gemv::resolve<DLK_EPI_SWIGLU>(p, mt);
+}
+
+dlk::gemv::Kernel dlk_gemm_kernel_swiglu(const dlk_gemv_params& p, int mt) {
+    return dlk::gemm::resolve<DLK_EPI_SWIGLU>(p, mt);
+}
+
+dlk::gemv::Kernel dlk_gemm_reduce_swiglu(const dlk_gemv_params& p) {
+    return dlk::gemm::resolve_reduce<DLK_EPI_SWIGLU>(p);
 }

@@ -80,7 +80,14 @@ typedef struct dlk_gemv_params {
     const int64_t* key_label; /* if set, the key is fold_in(key, *key_label) */
     dlk_sample_partial* partial; /* [M_total, blocks] */
     int partial_blocks;
+    /* Workspace for key-split launches of the matrix-core path (NULL: never split): partial dot products and
+     * per-row sums of squares of each key slice, reduced in fixed order by a second launch. */
+    float* split_partial;
+    int64_t split_capacity; /* floats */
 } dlk_gemv_params;
+
+/* Floats of workspace that lets dlk_gemv split the keys of this launch (0 when it would not split). */
+int64_t dlk_gemv_split_floats(const dlk_gemv_params* p);
 
 /* Work-groups of the persistent launch (the LOGITS partial row length: one sampling candidate per work-group);
    -1 when no kernel fits the parameters.  Depends on the current device's CU count and the kernel's occupancy. */

@@ -168,57 +168,60 @@ __global__ __launch_bounds__(kThreads) void sample_partials_kernel(const float* 
     }
 }
 
-// One work-group of 1024 threads reduces every row's candidates (the preference is associative and
-// commutative on distinct indices, so the reduction order does not change the result), then gathers the
-// chosen token's embedding row as the next step's input.
-constexpr int kFinalizeThreads = 1024;
+constexpr int kFinalizeThreads = 256;
+// One work-group per row: the row's candidates reduce with the preference rule (associative and commutative on
+// distinct indices, so the reduction order does not change the result; wave shuffles, then LDS), the
+// chosen id is written out, and its embedding row becomes the next step's input.  With `advance` (one row) the
+// work-group also advances the step counter; several rows leave that to step_advance_kernel, launched after,
+// so that no work-group reads the counter after another has written it.
 __global__ __launch_bounds__(kFinalizeThreads) void sample_finalize_kernel(
-    const dlk_sample_partial* partial, int64_t rows, int blocks, int64_t* out, int64_t* next_ids, int64_t* tokens,
-    int64_t token_stride, int64_t* step, const void* embedding, int embedding_dtype, int64_t width, float* x) {
+    const dlk_sample_partial* partial, int blocks, int64_t* out, int64_t* next_ids, int64_t* tokens,
+    int64_t token_stride, int64_t* step, int advance, const void* embedding, int embedding_dtype, int64_t width,
+    float* x) {
     __shared__ double wave_score[kFinalizeThreads / kWave];
     __shared__ int64_t wave_index[kFinalizeThreads / kWave];
     __shared__ int64_t chosen;
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int64_t row = blockIdx.x;
     const int64_t column = step ? *step : 0;
-    for (int64_t row = 0; row < rows; ++row) {
-        double best = 0.0;
-        int64_t index = -1;
-        for (int i = threadIdx.x; i < blocks; i += kFinalizeThreads) {
-            const dlk_sample_partial c = partial[row * blocks + i];
-            if (c.index < 0) continue;
-            if (index < 0 || prefer(c.score, c.index, best, index)) { best = c.score; index = c.index; }
-        }
-        for (int offset = kWave / 2; offset > 0; offset >>= 1) {
-            const double s = __shfl_xor(best, offset, kWave);
-            const int64_t j = __shfl_xor(index, offset, kWave);
-            if (j >= 0 && (index < 0 || prefer(s, j, best, index))) { best = s; index = j; }
-        }
-        if (lane == 0) { wave_score[wave] = best; wave_index[wave] = index; }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            double b = 0.0;
-            int64_t bi = -1;
-            for (int w = 0; w < kFinalizeThreads / kWave; ++w) {
-                const int64_t j = wave_index[w];
-                if (j >= 0 && (bi < 0 || prefer(wave_score[w], j, b, bi))) { b = wave_score[w]; bi = j; }
-            }
-            chosen = bi;
-            if (out) out[row] = bi;
-            if (next_ids) next_ids[row] = bi;
-            if (tokens) tokens[row * token_stride + column] = bi;
-        }
-        __syncthreads();
-        if (embedding && x) {
-            const int64_t id = chosen < 0 ? 0 : chosen;
-            for (int64_t i = threadIdx.x; i < width; i += kFinalizeThreads)
-                x[row * width + i] = embedding_dtype == DLK_BF16
-                                         ? bf16_to_f32(static_cast<const uint16_t*>(embedding)[id * width + i])
-                                         : static_cast<const float*>(embedding)[id * width + i];
-        }
-        __syncthreads();
+    double best = 0.0;
+    int64_t index = -1;
+    for (int i = threadIdx.x; i < blocks; i += kFinalizeThreads) {
+        const dlk_sample_partial c = partial[row * blocks + i];
+        if (c.index < 0) continue;
+        if (index < 0 || prefer(c.score, c.index, best, index)) { best = c.score; index = c.index; }
     }
-    if (step && threadIdx.x == 0) *step = column + 1;
+    for (int offset = kWave / 2; offset > 0; offset >>= 1) {
+        const double s = __shfl_xor(best, offset, kWave);
+        const int64_t j = __shfl_xor(index, offset, kWave);
+        if (j >= 0 && (index < 0 || prefer(s, j, best, index))) { best = s; index = j; }
+    }
+    if (lane == 0) { wave_score[wave] = best; wave_index[wave] = index; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double b = 0.0;
+        int64_t bi = -1;
+        for (int w = 0; w < kFinalizeThreads / kWave; ++w) {
+            const int64_t j = wave_index[w];
+            if (j >= 0 && (bi < 0 || prefer(wave_score[w], j, b, bi))) { b = wave_score[w]; bi = j; }
+        }
+        chosen = bi;
+        if (out) out[row] = bi;
+        if (next_ids) next_ids[row] = bi;
+        if (tokens) tokens[row * token_stride + column] = bi;
+    }
+    __syncthreads();
+    if (embedding && x) {
+        const int64_t id = chosen < 0 ? 0 : chosen;
+        for (int64_t i = threadIdx.x; i < width; i += kFinalizeThreads)
+            x[row * width + i] = embedding_dtype == DLK_BF16
+                                     ? bf16_to_f32(static_cast<const uint16_t*>(embedding)[id * width + i])
+                                     : static_cast<const float*>(embedding)[id * width + i];
+    }
+    if (advance && step && threadIdx.x == 0) *step = column + 1;
 }
+
+__global__ void step_advance_kernel(int64_t* step) { *step += 1; }
 
 // First maximum of one row per work-group (NaN first, ties to the lower index), reference
 // src/kernels/cpu/reduction.cpp:128-151.
@@ -382,10 +385,17 @@ int dlk_sample_partials(const float* logits, int64_t rows, int64_t n, int mode, 
 int dlk_sample_finalize(const dlk_sample_partial* partial, int64_t rows, int blocks, int64_t* out, int64_t* next_ids,
                         int64_t* tokens, int64_t token_stride, int64_t* step, const void* embedding,
                         int embedding_dtype, int64_t width, float* x, dlh_stream stream) {
-    hipLaunchKernelGGL(dlk::sample_finalize_kernel, dim3(1), dim3(dlk::kFinalizeThreads), 0, as_stream(stream),
-                       partial, rows, blocks, out, next_ids, tokens, token_stride, step, embedding, embedding_dtype,
-                       width, x);
-    return dlk::status();
+    if (rows <= 0) return 0;
+    const int advance = rows == 1;
+    hipLaunchKernelGGL(dlk::sample_finalize_kernel, dim3(static_cast<unsigned>(rows)), dim3(dlk::kFinalizeThreads), 0,
+                       as_stream(stream), partial, blocks, out, next_ids, tokens, token_stride, step, advance,
+                       embedding, embedding_dtype, width, x);
+    int status = dlk::status();
+    if (status == 0 && !advance && step) {
+        hipLaunchKernelGGL(dlk::step_advance_kernel, dim3(1), dim3(1), 0, as_stream(stream), step);
+        status = dlk::status();
+    }
+    return status;
 }
 
 int dlk_argmax(const float* x, int64_t rows, int64_t n, int64_t* out, dlh_stream stream) {

@@ -129,6 +129,13 @@ def test_operators_match_the_oracle():
     for weight, dtype in ((w, ct.F32), (wb, ct.BF16)):
         y = ct.linear(G(x), G(weight, dtype)).numpy()
         assert rel_err(y, oracle.linear(x, weight)) <= 1e-5
+    # several rows over bf16 weights with 16-row tiles take the matrix cores: activations split into bf16
+    # hi + lo (each product carries ~2^-17 relative error), so the bound is the f32 logit tolerance, 1e-4
+    for rows, n, k in ((5, 320, 2048), (37, 64, 512), (64, 48, 4096), (3, 16, 768)):
+        xx = rng.standard_normal((rows, k)).astype(np.float32)
+        ww = oracle.bf16_encode((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        yy = ct.linear(G(xx), G(ww, ct.BF16)).numpy()
+        assert rel_err(yy, oracle.linear(xx, ww)) <= 1e-4, (rows, n, k)
     # K not a multiple of the vector chunk takes the generic kernel
     xs = rng.standard_normal((3, 13)).astype(np.float32)
     ws = rng.standard_normal((7, 13)).astype(np.float32)
@@ -186,6 +193,29 @@ def test_batched_decode_over_a_seeded_prefix():
         got = gpu.logits(ids, gc)
         assert np.max(np.abs(got - want)) <= 2e-2, step
         ids = want.argmax(-1).reshape(B, 1)
+
+
+def test_batched_decode_on_matrix_cores():
+    say("case: B=6 bf16 decode, d=512 (projections on the matrix cores, key-split with a reduce launch)")
+    cfg = oracle.ModelConfig(vocab=1000, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=1376, context=48,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(47, 0), scale=0.05)
+    B = 6
+    prompt = oracle.random_ids((48, 0), B * 5, cfg.vocab).reshape(B, 5)
+    rc, gc = ref.make_cache(B), gpu.cache()
+    want = ref.logits(prompt, rc)[:, -1]
+    got = gpu.logits(prompt, gc)
+    assert np.max(np.abs(got - want)) <= 2e-2
+    ids = want.argmax(-1).reshape(B, 1)
+    for step in range(4):  # single-position steps: 6 activation rows per projection
+        want = ref.logits(ids, rc)[:, -1]
+        got = gpu.logits(ids, gc)
+        assert np.max(np.abs(got - want)) <= 2e-2, step
+        ids = want.argmax(-1).reshape(B, 1)
+    t1, l1 = gpu.generate(prompt, 10, 1.0, (3, 4), use_graph=True)
+    t2, l2 = gpu.generate(prompt, 10, 1.0, (3, 4), use_graph=False)
+    assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
+    assert np.array_equal(oracle.sample(l1, 1.0, oracle.fold_in((3, 4), 9)), t1[:, -1])
 
 
 def test_decode_over_split_keys_merges_partials():
