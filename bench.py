@@ -9,7 +9,8 @@ the GPU: embedding gather -> 16 fused layers -> final norm + LM head -> sampling
 HIP graph; exactly --steps steps are timed with HIP events on the library's compute stream after --warmup
 untimed steps.
 
-Also reported: the b=32 decode over a 2048-token seeded K/V prefix (configs[2], "C3"), the per-kernel roofline of
+Also reported: the b=32 decode over a 2048-token seeded K/V prefix (configs[2], "C3"), the 8B-class b=8 decode over
+a 32768-token seeded K/V prefix (configs[3], "C4"), the per-kernel roofline of
 the dominant kernel (gate/up projection: each layer's launch repeated back to back between two HIP events on the
 compute stream), a streaming-copy bandwidth reference, and the CPU oracle timed on this host (single thread) on
 a bounded sample of the same workload.
@@ -31,6 +32,7 @@ HBM_PEAK_GBPS = 8000.0
 # the traffic summary under profiles/.  A measurement of the kernel as built, not derived from the bytes below.
 GATE_UP_TRAFFIC_BYTES = 46.37e6 + 0.045e6
 C2 = dict(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632)
+C4 = dict(vocab=32000, layers=32, dimensions=4096, heads=32, kv_heads=8, hidden=14336, rope_base=500000.0)
 
 
 def log(msg):
@@ -57,7 +59,7 @@ def build_model(ct, cfg, context, root=(1234, 0)):
     """Seeded weights drawn directly in HBM: slot s gets 0.02 * randn(fold_in(root, s)) rounded to bf16."""
     gpu = ct.device("gpu")
     decoder = ct.transformer_decoder(cfg["layers"], cfg["dimensions"], cfg["heads"], cfg["kv_heads"], cfg["hidden"],
-                                     context, ct.BF16, gpu)
+                                     context, ct.BF16, gpu, cfg.get("rope_base", 10000.0))
     state, embedding, head = {}, None, None
     for slot, (name, shape) in enumerate(parameter_slots(cfg)):
         if name.endswith("norm.weight") or name == "decoder.normalization.weight":
@@ -125,6 +127,24 @@ def decode_b32(ct, steps, warmup, prefix=2048):
     return dict(ms=ms, step_bytes=weight_bytes(C2) + kv_bytes(C2, B, mean_len), batch=B, mean_len=mean_len)
 
 
+def decode_c4(ct, steps, warmup, batch=8, prefix=32768):
+    """C4: the 8B-class decoder (RoPE base 500000), batch 8, each sequence holding `prefix` cached positions of
+    seeded random K/V (34 GB of bf16 KV at 32768), greedy decode."""
+    cfg = C4
+    decoder, lm = build_model(ct, cfg, prefix + 3 + warmup + steps + 8, root=(88, 0))
+    cache = ct.DecoderCache(decoder)
+    hd = cfg["dimensions"] // cfg["heads"]
+    for layer in range(cfg["layers"]):
+        k = ct.normal(ct.fold_in((4343, 0), 2 * layer), [batch, cfg["kv_heads"], prefix, hd], 1.0, ct.BF16)
+        v = ct.normal(ct.fold_in((4343, 0), 2 * layer + 1), [batch, cfg["kv_heads"], prefix, hd], 1.0, ct.BF16)
+        cache.append(layer, k, v)
+        del k, v
+    ids = np.random.default_rng(9).integers(0, cfg["vocab"], size=(batch, 1), dtype=np.int64)
+    ms, _ = lm.benchmark(ids, cache, warmup, steps, 0.0, (0, 0), True)
+    mean_len = prefix + 3 + warmup + (steps - 1) / 2.0
+    return dict(ms=ms, step_bytes=weight_bytes(cfg) + kv_bytes(cfg, batch, mean_len), batch=batch, mean_len=mean_len)
+
+
 def cpu_baseline(prompt_len=4, decode_steps=8):
     """The CPU oracle (plain-C restatement of the reference CPU path) on this host, one thread, at the C2 shape:
     a short prompt is fed, then `decode_steps` single-token greedy steps are timed."""
@@ -158,6 +178,8 @@ def main():
     ap.add_argument("--b32-steps", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-b32", action="store_true")
+    ap.add_argument("--c4-steps", type=int, default=16)
+    ap.add_argument("--no-c4", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -184,9 +206,11 @@ def main():
                for t in b1["timings"]}
 
     extra = {}
+    del lm, decoder  # free the C2 model's HBM before the larger workloads
+    import gc
+    gc.collect()
     if not args.no_b32:
         log("bench: b=32 over a 2048-token prefix")
-        del lm, decoder
         b32 = decode_b32(ct, args.b32_steps, 4)
         ms32 = b32["ms"] / args.b32_steps
         extra["b32"] = {"tok_s": 32 * args.b32_steps / (b32["ms"] / 1e3), "ms_per_step": ms32,
@@ -194,6 +218,18 @@ def main():
                         "frac_of_peak": b32["step_bytes"] / (ms32 / 1e3) / 1e9 / HBM_PEAK_GBPS,
                         "steps": args.b32_steps, "prefix": 2048}
         log(f"bench: b=32 {ms32:.3f} ms/step, {extra['b32']['tok_s']:.0f} tok/s")
+
+    if not args.no_c4:
+        log("bench: C4 8B b=8 over a 32768-token prefix")
+        gc.collect()
+        c4 = decode_c4(ct, args.c4_steps, 2)
+        ms4 = c4["ms"] / args.c4_steps
+        extra["c4"] = {"tok_s": c4["batch"] * args.c4_steps / (c4["ms"] / 1e3), "ms_per_step": ms4,
+                       "achieved_GBps": c4["step_bytes"] / (ms4 / 1e3) / 1e9,
+                       "frac_of_peak": c4["step_bytes"] / (ms4 / 1e3) / 1e9 / HBM_PEAK_GBPS,
+                       "steps": args.c4_steps, "prefix": 32768, "batch": c4["batch"]}
+        log(f"bench: C4 {ms4:.2f} ms/step, {extra['c4']['tok_s']:.0f} tok/s, {extra['c4']['achieved_GBps']:.0f} GB/s")
+        del c4
 
     baseline = None
     if not args.no_cpu_baseline:

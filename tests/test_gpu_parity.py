@@ -218,6 +218,32 @@ def test_batched_decode_on_matrix_cores():
     assert np.array_equal(oracle.sample(l1, 1.0, oracle.fold_in((3, 4), 9)), t1[:, -1])
 
 
+def test_head_dim_128_batched_decode_over_a_long_prefix():
+    say("case: B=8 decode, head dim 128, RoPE base 500000, 1000-token seeded prefix (the C4 route at small scale)")
+    cfg = oracle.ModelConfig(vocab=1000, layers=2, dimensions=1024, heads=8, kv_heads=2, hidden=2048, context=1024,
+                             dtype="bf16", rope_base=500000.0)
+    ref, gpu = build_pair(cfg, root=(51, 0), scale=0.03)
+    B, P, hd = 8, 1000, cfg.head_dim
+    rc, gc = ref.make_cache(B), gpu.cache()
+    for layer in range(cfg.layers):
+        k = oracle.randn(oracle.fold_in((81, 0), 2 * layer), B * 2 * P * hd).reshape(B, 2, P, hd)
+        v = oracle.randn(oracle.fold_in((81, 0), 2 * layer + 1), B * 2 * P * hd).reshape(B, 2, P, hd)
+        kb, vb = oracle.bf16_encode(k), oracle.bf16_encode(v)
+        gc.append(layer, ct.Tensor.from_numpy(kb, ct.BF16, GPU), ct.Tensor.from_numpy(vb, ct.BF16, GPU))
+        rc.fill(layer, P, oracle.bf16_decode(kb), oracle.bf16_decode(vb))
+    ids = oracle.random_ids((82, 0), B, cfg.vocab).reshape(B, 1)
+    for step in range(3):
+        want = ref.logits(ids, rc)[:, -1]
+        got = gpu.logits(ids, gc)
+        assert np.max(np.abs(got - want)) <= 2e-2, step
+        ids = want.argmax(-1).reshape(B, 1)
+    gc.truncate(P)
+    t1, l1 = gpu.generate(ids, 6, 0.0, (0, 0), use_graph=True, cache=gc)
+    gc.truncate(P)
+    t2, l2 = gpu.generate(ids, 6, 0.0, (0, 0), use_graph=False, cache=gc)
+    assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
+
+
 def test_decode_over_split_keys_merges_partials():
     say("case: B=2 decode over a 600-token prefix, head dim 64, 4 query heads per KV head (2 key splits)")
     cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=512, context=640,
