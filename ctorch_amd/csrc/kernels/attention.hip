@@ -201,37 +201,45 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const dlk_attention
     }
 }
 
-// One wave per (b, h, l) row: merges the split partials with the usual max-rescaled weights.
+// One work-group per (b, h, l) row merges its split partials: the global maximum first, then each thread takes
+// one head-dim column and every (256 / HD)-th split, and the column groups add up in LDS in a fixed order.
 template <int HD>
-__global__ __launch_bounds__(kWave) void attention_combine(const dlk_attention_params p) {
-    constexpr int DCOLS = (HD + kWave - 1) / kWave;
+__global__ __launch_bounds__(kThreads) void attention_combine(const dlk_attention_params p) {
+    constexpr int GROUPS = kThreads / HD;
+    __shared__ float wave_max_s[kWaves];
+    __shared__ float acc_s[GROUPS][HD];
+    __shared__ float total_s[GROUPS];
     const int64_t prow = blockIdx.x; // (b * H + h) * L + l
-    const int lane = threadIdx.x;
+    const int t = threadIdx.x, lane = t % kWave;
     const int64_t l = prow % p.L, h = (prow / p.L) % p.H, b = prow / (static_cast<int64_t>(p.L) * p.H);
     const float* ml = p.partial_ml + prow * p.splits * 2;
     float maximum = -INFINITY;
-    for (int s = 0; s < p.splits; ++s) maximum = fmaxf(maximum, ml[2 * s]);
-    float total = 0.0f, acc[DCOLS];
-#pragma unroll
-    for (int c = 0; c < DCOLS; ++c) acc[c] = 0.0f;
-    for (int s = 0; s < p.splits; ++s) {
+    for (int s = t; s < p.splits; s += kThreads)
+        if (ml[2 * s + 1] > 0.0f) maximum = fmaxf(maximum, ml[2 * s]);
+    maximum = wave_max(maximum);
+    if (lane == 0) wave_max_s[t / kWave] = maximum;
+    __syncthreads();
+    maximum = fmaxf(fmaxf(wave_max_s[0], wave_max_s[1]), fmaxf(wave_max_s[2], wave_max_s[3]));
+    const int d = t % HD, group = t / HD;
+    float acc = 0.0f, total = 0.0f;
+    for (int s = group; s < p.splits; s += GROUPS) {
         const float ms = ml[2 * s], ls = ml[2 * s + 1];
-        if (ls <= 0.0f || ms == -INFINITY) continue;
-        const float w = expf(ms - maximum);
+        const float w = ls > 0.0f && ms != -INFINITY ? expf(ms - maximum) : 0.0f;
         total += w * ls;
-        const float* o = p.partial_o + (prow * p.splits + s) * HD;
-#pragma unroll
-        for (int c = 0; c < DCOLS; ++c) {
-            const int d = lane + c * kWave;
-            if (d < HD) acc[c] += w * o[d];
-        }
+        acc += w * p.partial_o[(prow * p.splits + s) * HD + d];
     }
-    const float inv = total > 0.0f ? 1.0f / total : 0.0f;
-    const int64_t m = b * p.L + l;
+    acc_s[group][d] = acc;
+    if (d == 0) total_s[group] = total;
+    __syncthreads();
+    if (group == 0) {
+        float sum = 0.0f, weight = 0.0f;
 #pragma unroll
-    for (int c = 0; c < DCOLS; ++c) {
-        const int d = lane + c * kWave;
-        if (d < HD) p.out[m * p.ldo + h * HD + d] = acc[c] * inv;
+        for (int g = 0; g < GROUPS; ++g) {
+            sum += acc_s[g][d];
+            weight += total_s[g];
+        }
+        const float inv = weight > 0.0f ? 1.0f / weight : 0.0f;
+        p.out[(b * p.L + l) * p.ldo + h * HD + d] = sum * inv;
     }
 }
 
@@ -371,7 +379,7 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
 
     // P*V: lane = (column pair lane % DL, key class lane / DL); the P values of the next PB keys are read from
     // LDS while the current ones are used
-    constexpr int PB = 8;
+    constexpr int PB = HD * G > 256 ? 4 : 8; // smaller batches keep the widest variants under 256 registers
     static_assert(VL % PB == 0, "P batches");
     float o[G][2];
 #pragma unroll
@@ -503,7 +511,7 @@ int launch_decode(const dlk_attention_params& p, hipStream_t stream) {
     }
     if (status != 0 || p.splits == 1 || p.partials_only) return status;
     const int64_t combine_rows = static_cast<int64_t>(p.B) * p.H;
-    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kWave), 0, stream, p);
+    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kThreads), 0, stream, p);
     return static_cast<int>(hipGetLastError());
 }
 
@@ -533,7 +541,7 @@ int launch(const dlk_attention_params& p, hipStream_t stream) {
     int status = static_cast<int>(hipGetLastError());
     if (status != 0 || p.splits == 1 || p.partials_only) return status;
     const int64_t combine_rows = static_cast<int64_t>(p.B) * p.H * p.L;
-    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kWave), 0, stream, p);
+    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kThreads), 0, stream, p);
     return static_cast<int>(hipGetLastError());
 }
 
