@@ -559,6 +559,7 @@ extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stre
         (p.splits > 1 && (!p.partial_o || !p.partial_ml)) || (p.splits > 1 && p.chunk % 64 != 0))
         return static_cast<int>(hipErrorInvalidValue);
     if (dlk::decode_path(p)) return p.hd == 64 ? dlk::launch_decode<64>(p, stream) : dlk::launch_decode<128>(p, stream);
+    if (dlk_attention_prefill_eligible(&p)) return dlk_attention_prefill(&p, stream_handle);
     if (p.kv_bf16) {
         switch (p.hd) {
         case 16: return dlk::launch<uint16_t, 16>(p, stream);

@@ -1,0 +1,250 @@
+// Causal grouped-query attention over a prefill chunk on the matrix cores (see dlk_attention_params in
+// kernels.h): bf16 K/V cache, head dim 64 or 128, one split.  Replaces, for L new positions, the query-blocked
+// grouped_block + attention_weights of the reference (src/ops/attention.cpp:59-95, 161-188): scores in f32,
+// causal rule key <= first + row (:52-57), softmax with the row maximum subtracted, P * V.
+//
+// Work-group: 4 waves and 128 query rows of one (batch, KV head): the G = H/KV query heads that share the KV
+// head times 128/G consecutive positions (row r -> head r / (128/G), position l0 + r % (128/G)); each wave owns
+// 32 rows as two 16-row query tiles.  Keys stream in tiles of 64 through LDS (double buffered: the next tile is
+// loaded into registers while the current one is used), K as loaded and V transposed, shared by every head of
+// the group.  Per tile and query tile:
+//   S^T[16 keys][16 queries] = K[16][HD] * Q[16][HD]^T   (v_mfma_f32_16x16x32_bf16; A = K rows from LDS,
+//                                                         B = the query rows, split into bf16 hi + lo)
+// so lane l holds S[keys 4(l/16) .. +4][query l%16]: the online softmax of query l%16 runs on the lane's own
+// values plus two cross-lane steps, and the probabilities of two adjacent 16-key tiles are already the B
+// operand of
+//   O^T[16 d][16 queries] += V^T[16 d][32 keys] * P^T     (A = V^T from the transposed LDS tile, in the key
+//                                                         order the lane holds; P split into hi + lo)
+// Two MFMAs per product (hi and lo) keep f32-level accuracy against the bf16 K and V.  Keys at or past the end
+// of the sequence are staged as zeros, so stale cache rows never reach the products.
+#include "kernels/device_common.h"
+
+namespace dlk {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRows = 128;  // query rows per work-group
+constexpr int kKeys = 64;   // keys per tile
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void split8(const f32x8 v, bf16x8& hi, bf16x8& lo) {
+    hi = __builtin_convertvector(v, bf16x8);
+    lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x8), bf16x8);
+}
+
+__device__ __forceinline__ void block_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int HD>
+__global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_attention_params p) {
+    constexpr int KS = HD / 32;                 // k steps of the score MFMA
+    constexpr int DT = HD / 16;                 // 16-wide head-dim tiles of the output
+    constexpr int KSTRIDE = HD + 8;             // bf16 per staged K row
+    constexpr int VSTRIDE = kKeys + 8;          // bf16 per staged V^T row (one head-dim column)
+    constexpr int CHUNKS = kKeys * HD / 8;      // 16-byte pieces of one K (or V) tile
+    constexpr int LOADS = CHUNKS / kThreads;    // per thread
+    static_assert(CHUNKS % kThreads == 0, "whole loads");
+    __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeys * KSTRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * VSTRIDE];
+
+    const int t = threadIdx.x, lane = t % kWave, q = lane / 16;
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int G = p.H / p.KV, per_head = kRows / G;
+    const int blocks = (p.L + per_head - 1) / per_head;
+    const int qb = blocks - 1 - static_cast<int>(blockIdx.x); // the longest key ranges start first
+    const int b = static_cast<int>(blockIdx.y) / p.KV, kvh = static_cast<int>(blockIdx.y) % p.KV;
+    const int64_t first = p.position ? *p.position : p.first_host;
+    const int64_t S = first + p.L;
+    const int l0 = qb * per_head;
+    const int64_t key_end = min(first + l0 + per_head, S); // keys any row of this work-group sees
+    const int tiles = static_cast<int>((key_end + kKeys - 1) / kKeys);
+
+    // this lane's two query rows (tile qt: row 32 wave + 16 qt + lane % 16)
+    int head[2], pos[2];
+    bool valid[2];
+    int64_t limit[2]; // last visible key
+    bf16x8 qh[2][KS], ql[2][KS];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int r = 32 * wave + 16 * qt + lane % 16;
+        head[qt] = kvh * G + r / per_head;
+        pos[qt] = l0 + r % per_head;
+        valid[qt] = pos[qt] < p.L;
+        const int l = min(pos[qt], p.L - 1);
+        limit[qt] = min(first + pos[qt], S - 1);
+        const float* row = p.q + (static_cast<int64_t>(b) * p.L + l) * p.ldq + static_cast<int64_t>(head[qt]) * HD;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const float4 a = *reinterpret_cast<const float4*>(row + 32 * s + 8 * q);
+            const float4 c = *reinterpret_cast<const float4*>(row + 32 * s + 8 * q + 4);
+            split8(f32x8{a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w}, qh[qt][s], ql[qt][s]);
+        }
+    }
+
+    // K/V staging: piece c = t + 256 i -> key c / (HD/8), head-dim group c % (HD/8)
+    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (static_cast<int64_t>(b) * p.KV + kvh) * p.capacity * HD;
+    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (static_cast<int64_t>(b) * p.KV + kvh) * p.capacity * HD;
+    u32x4 kr[LOADS], vr[LOADS];
+    auto load = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int c = t + kThreads * i, key = c / (HD / 8), dg = c % (HD / 8);
+            const int64_t k = static_cast<int64_t>(tile) * kKeys + key;
+            const int64_t row = min(k, S - 1); // in bounds; rows past the end are zeroed when staged
+            kr[i] = *reinterpret_cast<const u32x4*>(kbase + row * HD + 8 * dg);
+            vr[i] = *reinterpret_cast<const u32x4*>(vbase + row * HD + 8 * dg);
+        }
+    };
+    auto stage = [&](int tile, int buf) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int c = t + kThreads * i, key = c / (HD / 8), dg = c % (HD / 8);
+            const bool live = static_cast<int64_t>(tile) * kKeys + key < S;
+            const u32x4 kv = live ? kr[i] : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 vv = live ? vr[i] : u32x4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(&ks[buf][key * KSTRIDE + 8 * dg]) = kv;
+            const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vt[buf][(8 * dg + 2 * e) * VSTRIDE + key] = static_cast<uint16_t>(w[e] & 0xffffu);
+                vt[buf][(8 * dg + 2 * e + 1) * VSTRIDE + key] = static_cast<uint16_t>(w[e] >> 16);
+            }
+        }
+    };
+
+    f32x4 o[2][DT];
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[qt][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    load(0);
+    stage(0, 0);
+    block_barrier();
+    for (int tile = 0; tile < tiles; ++tile) {
+        const int buf = tile & 1;
+        if (tile + 1 < tiles) load(tile + 1);
+
+        // scores: s[i][qt] = S[keys 64 tile + 16 i + 4 q + j][query row (qt, lane % 16)]
+        f32x4 s[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) s[i][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < KS; ++st) {
+                const bf16x8 a =
+                    *reinterpret_cast<const bf16x8*>(&ks[buf][(16 * i + lane % 16) * KSTRIDE + 32 * st + 8 * q]);
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    s[i][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qh[qt][st], s[i][qt], 0, 0, 0);
+                    s[i][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ql[qt][st], s[i][qt], 0, 0, 0);
+                }
+            }
+        }
+
+        // online softmax per query row (the lane's column; lanes l, l^16, l^32, l^48 share it)
+        bf16x8 ph[2][2], pl[2][2]; // [key block u: tiles 2u, 2u+1][qt]
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t key = static_cast<int64_t>(tile) * kKeys + 16 * i + 4 * q + j;
+                    const float v = key <= limit[qt] ? s[i][qt][j] * p.scale : -INFINITY;
+                    s[i][qt][j] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            const float m_new = fmaxf(m_run[qt], mx);
+            const float alpha = m_run[qt] == -INFINITY ? 0.0f : expf(m_run[qt] - m_new);
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float e = s[i][qt][j] == -INFINITY ? 0.0f : expf(s[i][qt][j] - m_new);
+                    s[i][qt][j] = e;
+                    sum += e;
+                }
+            sum += __shfl_xor(sum, 16, kWave);
+            sum += __shfl_xor(sum, 32, kWave);
+            l_run[qt] = l_run[qt] * alpha + sum;
+            m_run[qt] = m_new;
+#pragma unroll
+            for (int d = 0; d < DT; ++d) o[qt][d] *= alpha;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                split8(f32x8{s[2 * u][qt][0], s[2 * u][qt][1], s[2 * u][qt][2], s[2 * u][qt][3],
+                             s[2 * u + 1][qt][0], s[2 * u + 1][qt][1], s[2 * u + 1][qt][2], s[2 * u + 1][qt][3]},
+                       ph[u][qt], pl[u][qt]);
+        }
+
+        // O^T += V^T P^T: lane (d = 16 dt + lane % 16, q) supplies V[keys 32 u + 4 q .. +4, 32 u + 16 + 4 q .. +4][d]
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const uint16_t* col = &vt[buf][(16 * dt + lane % 16) * VSTRIDE + 32 * u + 4 * q];
+                const u32x2 lo4 = *reinterpret_cast<const u32x2*>(col);
+                const u32x2 hi4 = *reinterpret_cast<const u32x2*>(col + 16);
+                const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[u][qt], o[qt][dt], 0, 0, 0);
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[u][qt], o[qt][dt], 0, 0, 0);
+                }
+            }
+        }
+
+        if (tile + 1 < tiles) stage(tile + 1, buf ^ 1);
+        block_barrier();
+    }
+
+    // lane holds O[query row (qt, lane % 16)][d = 16 dt + 4 q + j]
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        if (!valid[qt]) continue;
+        const float inv = 1.0f / l_run[qt];
+        float* out = p.out + (static_cast<int64_t>(b) * p.L + pos[qt]) * p.ldo + static_cast<int64_t>(head[qt]) * HD;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+            *reinterpret_cast<float4*>(out + 16 * dt + 4 * q) =
+                make_float4(o[qt][dt][0] * inv, o[qt][dt][1] * inv, o[qt][dt][2] * inv, o[qt][dt][3] * inv);
+    }
+}
+
+} // namespace
+} // namespace dlk
+
+/* Whether dlk_attention takes the matrix-core prefill kernel for these parameters. */
+extern "C" int dlk_attention_prefill_eligible(const dlk_attention_params* p) {
+    const int G = p->KV > 0 ? p->H / p->KV : 0;
+    return p->kv_bf16 && (p->hd == 64 || p->hd == 128) && p->L >= 16 && G > 0 && dlk::kRows % G == 0 &&
+           p->splits == 1 && p->ldq % 4 == 0 && p->ldo % 4 == 0;
+}
+
+extern "C" int dlk_attention_prefill(const dlk_attention_params* params, dlh_stream stream_handle) {
+    const dlk_attention_params& p = *params;
+    if (!dlk_attention_prefill_eligible(&p)) return static_cast<int>(hipErrorInvalidValue);
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
+    const int per_head = dlk::kRows / (p.H / p.KV);
+    const dim3 grid((p.L + per_head - 1) / per_head, p.B * p.KV);
+    if (p.hd == 64)
+        hipLaunchKernelGGL(dlk::attention_prefill<64>, grid, dim3(dlk::kThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL(dlk::attention_prefill<128>, grid, dim3(dlk::kThreads), 0, stream, p);
+    return static_cast<int>(hipGetLastError());
+}

@@ -376,8 +376,6 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
     }
 
     // epilogue: lane holds D[4q + j][m] of each activation tile
-    double best_score = 0.0;
-    int64_t best_index = -1;
     uint64_t seed = p.key_seed, stream = p.key_stream;
     if constexpr (EPI == DLK_EPI_LOGITS) {
         if (p.sample_mode == 2 && p.key_label)

@@ -1,10 +1,12 @@
 // Host dispatch of the projections: the GEMV (gemv_impl.h) for one or two activation rows (or shapes the matrix
-// cores do not take), the matrix-core kernel (gemm_rows.h) for more; both instantiated per epilogue in gemv_*.hip.
+// cores do not take), the matrix-core kernel (gemm_rows.h) for a batch of decode rows, and the tiled matrix-core
+// kernel (gemm_tiles.h) for prefill chunks large enough to fill the device; all instantiated per epilogue in
+// gemv_*.hip.
 //
 // The grid is persistent: one wave per row group, capped at the number of waves the chosen kernel keeps
 // resident on the device (its occupancy times the CU count), so every wave streams from the start and none
 // waits for another to retire.  LOGITS launches write one sampling candidate per work-group.
-#include "kernels/gemm_rows.h"
+#include "kernels/gemm_tiles.h"
 
 #include <mutex>
 #include <unordered_map>
@@ -46,6 +48,32 @@ Kernel resolve_reduce(const dlk_gemv_params& p) {
     case DLK_EPI_LOGITS: return dlk_gemm_reduce_logits(p);
     default: return {};
     }
+}
+
+Kernel resolve_tiles(const dlk_gemv_params& p) {
+    switch (p.epilogue) {
+    case DLK_EPI_STORE: return dlk_tiles_kernel_store(p);
+    case DLK_EPI_RESIDUAL: return dlk_tiles_kernel_residual(p);
+    case DLK_EPI_QKV: return dlk_tiles_kernel_qkv(p);
+    case DLK_EPI_SWIGLU: return dlk_tiles_kernel_swiglu(p);
+    default: return {};
+    }
+}
+
+// Tiled path: prepare_rows splits the activation rows into the staging workspace, then the tiled projection.
+int launch_tiles(const dlk_gemv_params& p, hipStream_t stream) {
+    using namespace dlk::tiles;
+    const Kernel kernel = resolve_tiles(p);
+    if (!kernel.fn) return static_cast<int>(hipErrorInvalidValue);
+    void* args[] = {const_cast<dlk_gemv_params*>(&p)};
+    const bool norm = p.apply_norm && p.epilogue != DLK_EPI_RESIDUAL;
+    const void* prep = norm ? reinterpret_cast<const void*>(&prepare_rows<true>)
+                            : reinterpret_cast<const void*>(&prepare_rows<false>);
+    hipError_t status = hipLaunchKernel(prep, dim3(p.M), dim3(kPrepThreads), args, 0, stream);
+    if (status != hipSuccess) return static_cast<int>(status);
+    const int blocks = col_blocks(p) * row_blocks(p);
+    status = hipLaunchKernel(kernel.fn, dim3(blocks), dim3(kThreads), args, kernel.lds, stream);
+    return static_cast<int>(status);
 }
 
 int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
@@ -123,9 +151,13 @@ int launch_waves(const dlk_gemv_params& p) {
 } // namespace
 
 extern "C" int64_t dlk_gemv_split_floats(const dlk_gemv_params* p) {
-    if (!dlk::gemm::eligible(*p)) return 0;
+    if (dlk::tiles::eligible(*p) || !dlk::gemm::eligible(*p)) return 0;
     const int rows = std::min(p->M, dlk::gemm::kMaxRows);
     return dlk::gemm::split_floats(*p, dlk::gemm::splits_of(*p, rows), rows);
+}
+
+extern "C" int64_t dlk_gemv_stage_bytes(const dlk_gemv_params* p) {
+    return dlk::tiles::shape_eligible(*p) ? dlk::tiles::stage_bytes(*p) : 0;
 }
 
 extern "C" int dlk_gemv_blocks(const dlk_gemv_params* p) {
@@ -149,6 +181,7 @@ extern "C" int dlk_gemv(const dlk_gemv_params* params, dlh_stream stream_handle)
     if (params->epilogue == DLK_EPI_QKV)
         for (int s = 0; s < params->nseg; ++s)
             if (params->seg_rows[s] % 2 != 0 || params->head_dim % 2 != 0) return static_cast<int>(hipErrorInvalidValue);
+    if (dlk::tiles::eligible(*params)) return launch_tiles(*params, stream);
     if (dlk::gemm::eligible(*params)) return launch_gemm(*params, stream);
     const int waves = launch_waves(*params);
     if (waves <= 0) return static_cast<int>(hipErrorInvalidValue);

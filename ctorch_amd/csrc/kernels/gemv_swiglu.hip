@@ -1,5 +1,5 @@
 // Projection kernels with the SWIGLU epilogue: the GEMV (one activation row) and the matrix-core variant.
-#include "kernels/gemm_rows.h"
+#include "kernels/gemm_tiles.h"
 
 dlk::gemv::Kernel dlk_gemv_kernel_swiglu(const dlk_gemv_params& p, int mt) {
     return dlk::gemv::resolve<DLK_EPI_SWIGLU>(p, mt);
@@ -11,4 +11,8 @@ dlk::gemv::Kernel dlk_gemm_kernel_swiglu(const dlk_gemv_params& p, int mt) {
 
 dlk::gemv::Kernel dlk_gemm_reduce_swiglu(const dlk_gemv_params& p) {
     return dlk::gemm::resolve_reduce<DLK_EPI_SWIGLU>(p);
+}
+
+dlk::gemv::Kernel dlk_tiles_kernel_swiglu(const dlk_gemv_params& p) {
+    return dlk::tiles::resolve<DLK_EPI_SWIGLU>(p);
 }

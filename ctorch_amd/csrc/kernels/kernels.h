@@ -84,10 +84,18 @@ typedef struct dlk_gemv_params {
      * per-row sums of squares of each key slice, reduced in fixed order by a second launch. */
     float* split_partial;
     int64_t split_capacity; /* floats */
+    /* Workspace of the tiled (prefill) path: a preparation launch writes the activation rows (times the norm
+     * weight) split into bf16 hi + lo rows and the per-row norm factors.  NULL: many-row launches take the
+     * batched matrix-core path (64 rows per launch) instead. */
+    void* stage;
+    int64_t stage_bytes;
 } dlk_gemv_params;
 
 /* Floats of workspace that lets dlk_gemv split the keys of this launch (0 when it would not split). */
 int64_t dlk_gemv_split_floats(const dlk_gemv_params* p);
+/* Bytes of staging workspace that lets this launch take the tiled (prefill) path: attach it as stage /
+   stage_bytes (0 when the shape does not suit that path). */
+int64_t dlk_gemv_stage_bytes(const dlk_gemv_params* p);
 
 /* Work-groups of the persistent launch (the LOGITS partial row length: one sampling candidate per work-group);
    -1 when no kernel fits the parameters.  Depends on the current device's CU count and the kernel's occupancy. */
@@ -130,6 +138,10 @@ int dlk_attention_decode_chunk(int heads, int kv_heads, int head_dim, int kv_bf1
 
 
 int dlk_attention(const dlk_attention_params* p, dlh_stream stream);
+/* The matrix-core causal prefill kernel (attention_prefill.hip), which dlk_attention takes for bf16 K/V, head
+   dim 64 or 128, L >= 16 new positions, one split and H/KV dividing 128. */
+int dlk_attention_prefill_eligible(const dlk_attention_params* p);
+int dlk_attention_prefill(const dlk_attention_params* p, dlh_stream stream);
 
 /* ------------------------------------------------------------------------------------------------------
  * Small kernels of the token loop and the tensor API.

@@ -43,7 +43,14 @@ void DecodeWorkspace::ensure(const TransformerDecoderLayer& layer, Index n, Inde
         lora_value = empty_tensor({n, va->rank()}, DType::f32, device);
 }
 
-void DecodeWorkspace::attach_split(dlk_gemv_params& p, Device device) {
+void DecodeWorkspace::attach_workspace(dlk_gemv_params& p, Device device) {
+    const int64_t stage_need = dlk_gemv_stage_bytes(&p);
+    if (stage_need > 0) {
+        if (!stage.defined() || stage.numel() * 4 < stage_need || !(stage.device() == device))
+            stage = empty_tensor({(stage_need + 3) / 4}, DType::f32, device);
+        p.stage = mutable_data(stage);
+        p.stage_bytes = stage.numel() * 4;
+    }
     const int64_t need = dlk_gemv_split_floats(&p);
     if (need <= 0) return;
     if (!split.defined() || split.numel() < need || !(split.device() == device))
@@ -145,7 +152,7 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
              attention.query_adapter()->scale() != attention.value_adapter()->scale()))
             throw std::invalid_argument("query and value adapters must share rank and alpha");
         const double bytes = static_cast<double>((H + 2 * KV) * hd * d) * (qb ? 2 : 4) + 2.0 * kv_bytes_per * length;
-        ws.attach_split(p, device);
+        ws.attach_workspace(p, device);
         issue(observer, "qkv_rope_append", bytes,
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "QKV projection"); });
     }
@@ -191,7 +198,7 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         p.ldres = d;
         p.bump_position = cache.position_data();
         p.bump_count = length;
-        ws.attach_split(p, device);
+        ws.attach_workspace(p, device);
         issue(observer, "output_residual", static_cast<double>(d * d) * (ob ? 2 : 4), [p, &context](bool repeat) {
             dlk_gemv_params q = p;
             if (repeat) q.bump_position = nullptr; // a timing repeat leaves the device length alone
@@ -215,7 +222,7 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         p.w_bf16 = gb;
         p.y = static_cast<float*>(mutable_data(ws.activation));
         p.ldy = F;
-        ws.attach_split(p, device);
+        ws.attach_workspace(p, device);
         issue(observer, "gate_up_silu", static_cast<double>(2 * F * d) * (gb ? 2 : 4),
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "gate/up projection"); });
     }
@@ -232,7 +239,7 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         p.ldy = d;
         p.residual = ws.hidden.data<float>();
         p.ldres = d;
-        ws.attach_split(p, device);
+        ws.attach_workspace(p, device);
         issue(observer, "down_residual", static_cast<double>(F * d) * (db ? 2 : 4),
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "down projection"); });
     }

@@ -16,8 +16,10 @@ struct DecodeWorkspace {
     Index rows = 0, splits_capacity = 0;
     Tensor q, attention, hidden, activation, partial_o, partial_ml, lora_query, lora_value;
     Tensor split; ///< key-split partials of the matrix-core projections (shared: launches are stream-ordered)
-    /// Points `p` at the split workspace when its launch would split the keys (grown as needed).
-    void attach_split(dlk_gemv_params& p, Device device);
+    Tensor stage; ///< prefill projections: activation rows split into bf16 hi + lo, per-row norm factors
+    /// Points `p` at the staging workspace when its shape takes the tiled prefill path and at the split
+    /// workspace when its launch would split the keys (both grown as needed).
+    void attach_workspace(dlk_gemv_params& p, Device device);
     void ensure(const nn::TransformerDecoderLayer& layer, Index rows, Index heads_total, Index hidden_features,
                 int splits, Device device);
 };

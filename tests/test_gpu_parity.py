@@ -271,6 +271,45 @@ def test_decode_over_split_keys_merges_partials():
     assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
 
 
+def test_prefill_on_tiled_matrix_cores_with_lora_and_causal_attention():
+    say("case: bf16 prefill B=2 x 2048, d=1024 (tiled projections + matrix-core causal attention), LoRA q/v")
+    cfg = oracle.ModelConfig(vocab=512, layers=1, dimensions=1024, heads=16, kv_heads=4, hidden=2816, context=2056,
+                             dtype="bf16", lora_rank=16, lora_alpha=32.0)
+    weights = oracle.synthesize_weights(cfg, (61, 0), 0.03)
+    # non-unit norm weights so the fused norm-weight path is exercised; bf16 values, since a bf16 decoder keeps
+    # its norm weights in bf16 (the reference creates every parameter in the module's dtype)
+    for i, name in enumerate(n for n in weights if n.endswith("norm.weight")):
+        g = (1.0 + 0.2 * oracle.randn((63, i), cfg.dimensions)).astype(np.float32)
+        weights[name] = oracle.bf16_decode(oracle.bf16_encode(g))
+    ref, gpu = build_pair(cfg, weights=weights)
+    B, P = 2, 2048
+    prompt = oracle.random_ids((62, 0), B * P, cfg.vocab).reshape(B, P)
+    rc, gc = ref.make_cache(B), gpu.cache()
+    want = ref.logits(prompt, rc)[:, -1]
+    got = gpu.logits(prompt, gc)
+    say(f"  prefill logits: max|d| {np.max(np.abs(got - want)):.3g}, rel {rel_err(got, want):.3g}")
+    # bf16 criterion (2e-2 max-abs); the hi + lo activations keep the gap far below it (bf16 K/V rounding of
+    # values computed in a different order is what remains)
+    assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4
+    ids = want.argmax(-1).reshape(B, 1)
+    for step in range(2):  # decode over the 2048 keys the tiled QKV epilogue wrote
+        want = ref.logits(ids, rc)[:, -1]
+        got = gpu.logits(ids, gc)
+        assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4, step
+        ids = want.argmax(-1).reshape(B, 1)
+    # two chunks of 1024 (the second attends with an offset) equal the single chunk
+    full = gpu.logits(prompt, gpu.cache())
+    chunked_cache = gpu.cache()
+    gpu.logits(prompt[:, :1024], chunked_cache)
+    chunked = gpu.logits(prompt[:, 1024:], chunked_cache)
+    assert rel_err(chunked, full) <= 1e-4
+    # a truncated cache prefilled again from position 1500 (548 rows: the batched projection path, attention
+    # with an offset) equals the single chunk
+    chunked_cache.truncate(1500)
+    again = gpu.logits(prompt[:, 1500:], chunked_cache)
+    assert rel_err(again, full) <= 1e-4
+
+
 # ------------------------------------------------------------------------------------------ C2 shape
 def test_c2_1b_shape_bf16_decode_parity():
     say("case: C2 1B bf16 shape (16 layers, d=2048, 32/8 heads, F=5632, V=32000), prompt 8 + 4 steps")
