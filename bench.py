@@ -33,6 +33,8 @@ HBM_PEAK_GBPS = 8000.0
 GATE_UP_TRAFFIC_BYTES = 46.37e6 + 0.045e6
 C2 = dict(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632)
 C4 = dict(vocab=32000, layers=32, dimensions=4096, heads=32, kv_heads=8, hidden=14336, rope_base=500000.0)
+C5 = dict(C2, lora_rank=16, lora_alpha=32.0)
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def log(msg):
@@ -47,8 +49,14 @@ def parameter_slots(cfg):
     for i in range(cfg["layers"]):
         p = f"decoder.layer{i}."
         names += [(p + "attention.query.weight", (H * hd, d)), (p + "attention.key.weight", (KV * hd, d)),
-                  (p + "attention.value.weight", (KV * hd, d)), (p + "attention.output.weight", (d, H * hd)),
-                  (p + "feedforward.gate.weight", (F, d)), (p + "feedforward.up.weight", (F, d)),
+                  (p + "attention.value.weight", (KV * hd, d)), (p + "attention.output.weight", (d, H * hd))]
+        if cfg.get("lora_rank"):
+            r = cfg["lora_rank"]
+            names += [(p + "attention.query_adapter.down.weight", (r, d)),
+                      (p + "attention.query_adapter.up.weight", (H * hd, r)),
+                      (p + "attention.value_adapter.down.weight", (r, d)),
+                      (p + "attention.value_adapter.up.weight", (KV * hd, r))]
+        names += [(p + "feedforward.gate.weight", (F, d)), (p + "feedforward.up.weight", (F, d)),
                   (p + "feedforward.down.weight", (d, F)), (p + "attention_norm.weight", (d,)),
                   (p + "feedforward_norm.weight", (d,))]
     names += [("decoder.normalization.weight", (d,)), ("output.weight", (V, d))]
@@ -56,15 +64,19 @@ def parameter_slots(cfg):
 
 
 def build_model(ct, cfg, context, root=(1234, 0)):
-    """Seeded weights drawn directly in HBM: slot s gets 0.02 * randn(fold_in(root, s)) rounded to bf16."""
+    """Seeded weights drawn directly in HBM: slot s gets 0.02 * randn(fold_in(root, s)) rounded to bf16 (LoRA up
+    matrices 1e-3 * randn); unmerged LoRA adapters on q and v when cfg has lora_rank."""
     gpu = ct.device("gpu")
     decoder = ct.transformer_decoder(cfg["layers"], cfg["dimensions"], cfg["heads"], cfg["kv_heads"], cfg["hidden"],
                                      context, ct.BF16, gpu, cfg.get("rope_base", 10000.0))
+    if cfg.get("lora_rank"):
+        ct.check(ct.lib().dl_transformer_decoder_attach_lora(decoder.handle, cfg["lora_rank"], cfg["lora_alpha"], 1, 1))
     state, embedding, head = {}, None, None
     for slot, (name, shape) in enumerate(parameter_slots(cfg)):
         if name.endswith("norm.weight") or name == "decoder.normalization.weight":
             continue  # RMSNorm weights keep their module default (ones)
-        w = ct.normal(ct.fold_in(root, slot), shape, 0.02, ct.BF16, gpu)
+        scale = 1e-3 if name.endswith("_adapter.up.weight") else 0.02
+        w = ct.normal(ct.fold_in(root, slot), shape, scale, ct.BF16, gpu)
         if name == "tokens.weight":
             embedding = w
         elif name == "output.weight":
@@ -145,6 +157,41 @@ def decode_c4(ct, steps, warmup, batch=8, prefix=32768):
     return dict(ms=ms, step_bytes=weight_bytes(cfg) + kv_bytes(cfg, batch, mean_len), batch=batch, mean_len=mean_len)
 
 
+def prefill_flops(cfg, batch, length):
+    """Algorithmic FLOPs of a prefill chunk: 2 * (decoder linear + LoRA parameters) per token, causal QK^T and PV
+    (4 * hd per visible query-key pair), and the LM head on the last position of each sequence."""
+    d, H, KV, F, V = cfg["dimensions"], cfg["heads"], cfg["kv_heads"], cfg["hidden"], cfg["vocab"]
+    hd = d // H
+    linear = (H * hd + 2 * KV * hd) * d + d * H * hd + 3 * F * d
+    if cfg.get("lora_rank"):
+        r = cfg["lora_rank"]
+        linear += r * d + H * hd * r + r * d + KV * hd * r
+    pairs = length * (length + 1) / 2
+    return (2.0 * cfg["layers"] * linear * batch * length + 4.0 * cfg["layers"] * batch * H * hd * pairs
+            + 2.0 * batch * V * d)
+
+
+def prefill_c5(ct, decode_steps, batch=4, length=4096):
+    """C5: the 1B-class decoder with unmerged LoRA (r=16, alpha=32) on q and v; prefill of `batch` x `length`
+    uniform random ids (timed with HIP events on the compute stream, after one untimed prefill), then greedy
+    decode of `decode_steps` tokens from the HIP graph."""
+    decoder, lm = build_model(ct, C5, length + decode_steps + 16, root=(555, 0))
+    prompt = np.random.default_rng(10).integers(0, C5["vocab"], size=(batch, length), dtype=np.int64)
+    cache = ct.DecoderCache(decoder)
+    lm.logits(prompt, cache)  # untimed: workspaces, first-touch
+    cache.truncate(0)
+    timer = ct.Timer()
+    timer.start()
+    logits = lm.logits(prompt, cache)
+    prefill_ms = timer.stop()
+    ids = logits.argmax(-1).reshape(batch, 1).astype(np.int64)
+    ms, _ = lm.benchmark(ids, cache, 2, decode_steps, 0.0, (0, 0), True)
+    flops = prefill_flops(C5, batch, length)
+    mean_len = length + 3 + (decode_steps - 1) / 2.0
+    return dict(prefill_ms=prefill_ms, flops=flops, decode_ms=ms, batch=batch, length=length,
+                step_bytes=weight_bytes(C5) + kv_bytes(C5, batch, mean_len))
+
+
 def cpu_baseline(prompt_len=4, decode_steps=8):
     """The CPU oracle (plain-C restatement of the reference CPU path) on this host, one thread, at the C2 shape:
     a short prompt is fed, then `decode_steps` single-token greedy steps are timed."""
@@ -180,6 +227,8 @@ def main():
     ap.add_argument("--no-b32", action="store_true")
     ap.add_argument("--c4-steps", type=int, default=16)
     ap.add_argument("--no-c4", action="store_true")
+    ap.add_argument("--c5-steps", type=int, default=128)
+    ap.add_argument("--no-c5", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -230,6 +279,22 @@ def main():
                        "steps": args.c4_steps, "prefix": 32768, "batch": c4["batch"]}
         log(f"bench: C4 {ms4:.2f} ms/step, {extra['c4']['tok_s']:.0f} tok/s, {extra['c4']['achieved_GBps']:.0f} GB/s")
         del c4
+
+    if not args.no_c5:
+        log("bench: C5 prefill 4 x 4096 with LoRA, then decode")
+        gc.collect()
+        c5 = prefill_c5(ct, args.c5_steps)
+        tflops = c5["flops"] / (c5["prefill_ms"] / 1e3) / 1e12
+        ms5 = c5["decode_ms"] / args.c5_steps
+        extra["c5"] = {"prefill_tok_s": c5["batch"] * c5["length"] / (c5["prefill_ms"] / 1e3),
+                       "prefill_ms": c5["prefill_ms"], "prefill_TFLOPs": tflops,
+                       "mfma_utilisation": tflops / MFMA_BF16_PEAK_TFLOPS, "prefill_flops": c5["flops"],
+                       "decode_tok_s": c5["batch"] * args.c5_steps / (c5["decode_ms"] / 1e3), "decode_ms_per_step": ms5,
+                       "decode_steps": args.c5_steps, "batch": c5["batch"], "prompt": c5["length"],
+                       "lora": "r=16, alpha=32 on q and v (unmerged)"}
+        log(f"bench: C5 prefill {c5['prefill_ms']:.1f} ms ({extra['c5']['prefill_tok_s']:.0f} tok/s, "
+            f"{tflops:.0f} TFLOP/s), decode {ms5:.3f} ms/step")
+        del c5
 
     baseline = None
     if not args.no_cpu_baseline:

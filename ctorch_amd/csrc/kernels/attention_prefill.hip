@@ -15,9 +15,13 @@
 // operand of
 //   O^T[16 d][16 queries] += V^T[16 d][32 keys] * P^T     (A = V^T from the transposed LDS tile, in the key
 //                                                         order the lane holds; P split into hi + lo)
-// Two MFMAs per product (hi and lo) keep f32-level accuracy against the bf16 K and V.  Keys at or past the end
-// of the sequence are staged as zeros, so stale cache rows never reach the products.
+// Two MFMAs per product (hi and lo) keep f32-level accuracy against the bf16 K and V.  The softmax runs in base 2
+// (log2 e folded into the score scale, one v_exp_f32 per score) and masks only the tiles that cross the causal
+// diagonal.  Keys at or past the end of the sequence are staged as zeros, so stale cache rows never reach the
+// products.
 #include "kernels/device_common.h"
+
+#include <type_traits>
 
 namespace dlk {
 namespace {
@@ -51,7 +55,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
     constexpr int VSTRIDE = kKeys + 8;          // bf16 per staged V^T row (one head-dim column)
     constexpr int CHUNKS = kKeys * HD / 8;      // 16-byte pieces of one K (or V) tile
     constexpr int LOADS = CHUNKS / kThreads;    // per thread
-    static_assert(CHUNKS % kThreads == 0, "whole loads");
+    static_assert(CHUNKS % kThreads == 0 && LOADS % 2 == 0, "whole loads; V pieces come in key pairs");
     __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeys * KSTRIDE];
     __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * VSTRIDE];
 
@@ -61,16 +65,18 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
     const int blocks = (p.L + per_head - 1) / per_head;
     const int qb = blocks - 1 - static_cast<int>(blockIdx.x); // the longest key ranges start first
     const int b = static_cast<int>(blockIdx.y) / p.KV, kvh = static_cast<int>(blockIdx.y) % p.KV;
-    const int64_t first = p.position ? *p.position : p.first_host;
-    const int64_t S = first + p.L;
+    const int first = static_cast<int>(p.position ? *p.position : p.first_host);
+    const int S = first + p.L;
     const int l0 = qb * per_head;
-    const int64_t key_end = min(first + l0 + per_head, S); // keys any row of this work-group sees
-    const int tiles = static_cast<int>((key_end + kKeys - 1) / kKeys);
+    const int key_end = min(first + l0 + per_head, S); // keys any row of this work-group sees
+    const int tiles = (key_end + kKeys - 1) / kKeys;
+    const int unmasked = (first + l0 + 1) / kKeys;      // tiles every row sees whole
+    const float scale2 = p.scale * 1.4426950408889634f; // scores in base 2
 
     // this lane's two query rows (tile qt: row 32 wave + 16 qt + lane % 16)
     int head[2], pos[2];
     bool valid[2];
-    int64_t limit[2]; // last visible key
+    int limit[2]; // last visible key
     bf16x8 qh[2][KS], ql[2][KS];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
@@ -85,37 +91,54 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
         for (int s = 0; s < KS; ++s) {
             const float4 a = *reinterpret_cast<const float4*>(row + 32 * s + 8 * q);
             const float4 c = *reinterpret_cast<const float4*>(row + 32 * s + 8 * q + 4);
-            split8(f32x8{a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w}, qh[qt][s], ql[qt][s]);
+            // the score scale (and log2 e) folded into the query before its split: the scores come out in base 2
+            split8(f32x8{a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w} * scale2, qh[qt][s], ql[qt][s]);
         }
     }
 
-    // K/V staging: piece c = t + 256 i -> key c / (HD/8), head-dim group c % (HD/8)
+    // K staging: piece c = t + 256 i -> key c / (HD/8), head-dim group c % (HD/8), stored as loaded.  V staging:
+    // lane -> key pair kp = lane % 32 and head-dim group 2 wave + lane / 32 (+ 8 per pass): the two keys' pieces
+    // are transposed into 32-bit words (key pair) of the V^T rows, the 64 lanes of a wave hitting 64 banks.
     const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (static_cast<int64_t>(b) * p.KV + kvh) * p.capacity * HD;
     const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (static_cast<int64_t>(b) * p.KV + kvh) * p.capacity * HD;
+    const int kp = lane % 32;
     u32x4 kr[LOADS], vr[LOADS];
     auto load = [&](int tile) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const int c = t + kThreads * i, key = c / (HD / 8), dg = c % (HD / 8);
-            const int64_t k = static_cast<int64_t>(tile) * kKeys + key;
-            const int64_t row = min(k, S - 1); // in bounds; rows past the end are zeroed when staged
-            kr[i] = *reinterpret_cast<const u32x4*>(kbase + row * HD + 8 * dg);
-            vr[i] = *reinterpret_cast<const u32x4*>(vbase + row * HD + 8 * dg);
+            const int row = min(tile * kKeys + key, S - 1); // in bounds; rows past the end are zeroed when staged
+            kr[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(row) * HD + 8 * dg);
+        }
+#pragma unroll
+        for (int i = 0; i < LOADS / 2; ++i) {
+            const int dg = 2 * wave + lane / 32 + 8 * i;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int row = min(tile * kKeys + 2 * kp + e, S - 1);
+                vr[2 * i + e] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(row) * HD + 8 * dg);
+            }
         }
     };
     auto stage = [&](int tile, int buf) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const int c = t + kThreads * i, key = c / (HD / 8), dg = c % (HD / 8);
-            const bool live = static_cast<int64_t>(tile) * kKeys + key < S;
-            const u32x4 kv = live ? kr[i] : u32x4{0u, 0u, 0u, 0u};
-            const u32x4 vv = live ? vr[i] : u32x4{0u, 0u, 0u, 0u};
-            *reinterpret_cast<u32x4*>(&ks[buf][key * KSTRIDE + 8 * dg]) = kv;
-            const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+            const bool live = tile * kKeys + key < S;
+            *reinterpret_cast<u32x4*>(&ks[buf][key * KSTRIDE + 8 * dg]) = live ? kr[i] : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < LOADS / 2; ++i) {
+            const int dg = 2 * wave + lane / 32 + 8 * i;
+            const bool live0 = tile * kKeys + 2 * kp < S, live1 = tile * kKeys + 2 * kp + 1 < S;
+            const u32x4 v0 = live0 ? vr[2 * i] : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 v1 = live1 ? vr[2 * i + 1] : u32x4{0u, 0u, 0u, 0u};
+            const uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w}, c[4] = {v1.x, v1.y, v1.z, v1.w};
+            uint32_t* col = reinterpret_cast<uint32_t*>(&vt[buf][8 * dg * VSTRIDE + 2 * kp]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                vt[buf][(8 * dg + 2 * e) * VSTRIDE + key] = static_cast<uint16_t>(w[e] & 0xffffu);
-                vt[buf][(8 * dg + 2 * e + 1) * VSTRIDE + key] = static_cast<uint16_t>(w[e] >> 16);
+                col[(2 * e) * (VSTRIDE / 2)] = (a[e] & 0xffffu) | (c[e] << 16);        // head-dim 8 dg + 2 e
+                col[(2 * e + 1) * (VSTRIDE / 2)] = (a[e] >> 16) | (c[e] & 0xffff0000u); // head-dim 8 dg + 2 e + 1
             }
         }
     };
@@ -127,10 +150,9 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
 #pragma unroll
         for (int d = 0; d < DT; ++d) o[qt][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    load(0);
-    stage(0, 0);
-    block_barrier();
-    for (int tile = 0; tile < tiles; ++tile) {
+    // one key tile; MASK: the tile crosses the causal diagonal of some row of the work-group
+    auto step = [&](int tile, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         const int buf = tile & 1;
         if (tile + 1 < tiles) load(tile + 1);
 
@@ -152,7 +174,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
             }
         }
 
-        // online softmax per query row (the lane's column; lanes l, l^16, l^32, l^48 share it)
+        // online softmax per query row (the lane's column; lanes l, l^16, l^32, l^48 share it), in base 2
         bf16x8 ph[2][2], pl[2][2]; // [key block u: tiles 2u, 2u+1][qt]
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
@@ -161,21 +183,24 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int64_t key = static_cast<int64_t>(tile) * kKeys + 16 * i + 4 * q + j;
-                    const float v = key <= limit[qt] ? s[i][qt][j] * p.scale : -INFINITY;
-                    s[i][qt][j] = v;
+                    float v = s[i][qt][j];
+                    if constexpr (MASK) {
+                        if (tile * kKeys + 16 * i + 4 * q + j > limit[qt]) v = -INFINITY;
+                        s[i][qt][j] = v;
+                    }
                     mx = fmaxf(mx, v);
                 }
             mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
             mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            // key 0 is visible to every row, so m_new is finite from the first tile on; exp2(-inf) = 0
             const float m_new = fmaxf(m_run[qt], mx);
-            const float alpha = m_run[qt] == -INFINITY ? 0.0f : expf(m_run[qt] - m_new);
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
             float sum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float e = s[i][qt][j] == -INFINITY ? 0.0f : expf(s[i][qt][j] - m_new);
+                    const float e = __builtin_amdgcn_exp2f(s[i][qt][j] - m_new);
                     s[i][qt][j] = e;
                     sum += e;
                 }
@@ -183,8 +208,10 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
             sum += __shfl_xor(sum, 32, kWave);
             l_run[qt] = l_run[qt] * alpha + sum;
             m_run[qt] = m_new;
+            if (!__all(alpha == 1.0f)) { // the running maxima of the wave's rows moved
 #pragma unroll
-            for (int d = 0; d < DT; ++d) o[qt][d] *= alpha;
+                for (int d = 0; d < DT; ++d) o[qt][d] *= alpha;
+            }
 #pragma unroll
             for (int u = 0; u < 2; ++u)
                 split8(f32x8{s[2 * u][qt][0], s[2 * u][qt][1], s[2 * u][qt][2], s[2 * u][qt][3],
@@ -211,7 +238,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
 
         if (tile + 1 < tiles) stage(tile + 1, buf ^ 1);
         block_barrier();
-    }
+    };
+    load(0);
+    stage(0, 0);
+    block_barrier();
+    for (int tile = 0; tile < min(unmasked, tiles); ++tile) step(tile, std::false_type{});
+    for (int tile = unmasked; tile < tiles; ++tile) step(tile, std::true_type{});
 
     // lane holds O[query row (qt, lane % 16)][d = 16 dt + 4 q + j]
 #pragma unroll

@@ -108,12 +108,20 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) 
     lo = f32_to_bf16(v - bf16_to_f32(hi));
 }
 
+// LoRA products of a lane's four tile rows, when the caller computed them (passed by value: a pointer to a
+// local array would keep it in scratch memory).
+struct LoraProducts {
+    float v[4];
+    bool set;
+};
+
 // The epilogue of one lane: v[j] = finished dot products of tile rows 4q + j (q = lane / 16) for activation
-// row m of the launch.
+// row m of the launch.  QKV: lora (if set) holds the unscaled LoRA products up[n, :] . hidden[m, :] of the
+// same rows, computed by the caller; otherwise they are computed here.
 template <int EPI>
 __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const TileMap& t, int q, int m,
                                               const float (&v)[4], double& best_score, int64_t& best_index,
-                                              uint64_t seed, uint64_t stream) {
+                                              uint64_t seed, uint64_t stream, LoraProducts lora = {{}, false}) {
     using Traits = gemv::WeightTraits<uint16_t>;
     if constexpr (EPI == DLK_EPI_SWIGLU) {
         const int n = t.n0 + 2 * q;
@@ -143,7 +151,10 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
         for (int pair = 0; pair < 2; ++pair) {
             const int n = t.n0 + 4 * q + 2 * pair; // even: the pair (n, n + 1) shares one rotation
             float even = v[2 * pair], odd = v[2 * pair + 1];
-            if (hidden) {
+            if (hidden && lora.set) {
+                even += lora.v[2 * pair] * p.lora_scale;
+                odd += lora.v[2 * pair + 1] * p.lora_scale;
+            } else if (hidden) {
                 // unmerged LoRA: + scale * up[n, :] . hidden[m, :]
                 const float* hrow = hidden + mg * p.lora_rank;
                 float de = 0.0f, dodd = 0.0f;

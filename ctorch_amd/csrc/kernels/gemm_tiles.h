@@ -45,7 +45,7 @@ constexpr int kActBytes = (kBM / 16) * 2048;       // one k step of activation f
 constexpr int kStageBytes = kWeightBytes + kActBytes;
 constexpr size_t kLdsBytes = 0;                    // the ring is static LDS
 constexpr int kDmaPerStep = (kBN / 16 + 2 * (kBM / 16)) / kWaves; // DMA instructions per wave per k step
-constexpr int kMinBlocks = 64;                     // smaller launches go to gemm_rows
+constexpr int kMinBlocks = 64;                     // one row block of 256 takes the tiled path only this wide
 constexpr int kXcds = 8;
 static_assert(kDmaPerStep == 6, "two weight tiles and two activation tiles (hi, lo) per wave");
 
@@ -62,14 +62,15 @@ __host__ __device__ inline int col_blocks(const dlk_gemv_params& p) {
 __host__ __device__ inline int row_blocks(const dlk_gemv_params& p) { return (p.M + kBM - 1) / kBM; }
 
 /// Whether the shape suits the tiled path (host side): bf16 weights, whole k steps, tile-shaped segments, rows
-/// that prepare_rows reads as float4, and enough work-groups.
+/// that prepare_rows reads as float4, and two or more row blocks (or one with a wide weight): narrower launches of
+/// that many rows would take gemm_rows 64 rows at a time, re-streaming the weights and under-filling the device.
 inline bool shape_eligible(const dlk_gemv_params& p) {
     if (!p.w_bf16 || p.epilogue == DLK_EPI_LOGITS || p.K % 32 != 0 || p.M < kBM) return false;
     if (p.ldx % 4 != 0 || reinterpret_cast<uintptr_t>(p.x) % 16 != 0) return false;
     if (static_cast<int64_t>(kBM) * p.K * 2 >= (int64_t(1) << 31)) return false; // 32-bit DMA lane offsets
     for (int s = 0; s < p.nseg; ++s)
         if (p.seg_rows[s] % gemm::kTile != 0) return false;
-    return static_cast<int64_t>(col_blocks(p)) * row_blocks(p) >= kMinBlocks;
+    return row_blocks(p) >= 2 || col_blocks(p) >= kMinBlocks;
 }
 
 /// The tiled path runs when the shape suits it and the caller attached the staging workspace.
@@ -248,6 +249,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
+            // weight tiles past the end (a narrow launch) hold repeats of the last tile: no products for them
+            if (!SWIGLU && 16 * n_blk + slot_tile(i) >= tiles) continue;
             const bf16x8 a = *reinterpret_cast<const bf16x8*>(base + slot_tile(i) * 1024 + 16 * lane);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -299,21 +302,60 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
             }
         }
     } else {
+        // QKV with LoRA of rank <= 32 (a multiple of 8): the rank-r products up[n, :] . hidden[m, :] of each output
+        // tile are one more pair of MFMAs, with A = the tile's up rows (k padded with zeros to 32) and B = the
+        // hidden rows split into hi + lo; D lands in the accumulator layout
+        const bool lora_mfma = EPI == DLK_EPI_QKV && p.lora_rank > 0 && p.lora_rank <= 32 && p.lora_rank % 8 == 0;
+        const bool lane_k = 8 * q < p.lora_rank; // lanes whose k slots hold rank entries
+        // fully unrolled: acc is only ever indexed with constants (a runtime index puts it in scratch memory)
+#pragma clang loop unroll(full)
+        for (int j = 0; j < 4; ++j) {
+            const int ml = 64 * wm + 16 * j + lane % 16, m = m_first + ml;
+            const float scale = inv[j] * p.acc_scale;
+            // hidden fragments of segments 0 (q) and 2 (v); the kernel-argument arrays and these are only indexed
+            // with constants or selects (a runtime index would copy them to scratch memory)
+            bf16x8 hh[2] = {}, hl[2] = {};
+            if constexpr (EPI == DLK_EPI_QKV) {
+                if (lora_mfma) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int tile = 16 * n_blk + 8 * wn + i;
-            if (tile >= tiles) continue;
-            const gemm::TileMap tm = gemm::locate<false>(p, tile);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int m = m_first + 64 * wm + 16 * j + lane % 16;
-                if (m >= p.M) continue;
-                const float scale = inv[j] * p.acc_scale;
+                    for (int h = 0; h < 2; ++h) {
+                        const float* hidden = h == 0 ? p.lora_hidden[0] : p.lora_hidden[2];
+                        if (!hidden) continue;
+                        const float* row = hidden + (p.m_base + min(m, p.M - 1)) * p.lora_rank + 8 * (lane_k ? q : 0);
+                        const float4 a = *reinterpret_cast<const float4*>(row);
+                        const float4 c = *reinterpret_cast<const float4*>(row + 4);
+                        f32x8 x = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+                        if (!lane_k) x = f32x8{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                        hh[h] = __builtin_convertvector(x, bf16x8);
+                        hl[h] = __builtin_convertvector(x - __builtin_convertvector(hh[h], f32x8), bf16x8);
+                    }
+                }
+            }
+#pragma clang loop unroll(full)
+            for (int i = 0; i < 8; ++i) {
+                const int tile = 16 * n_blk + 8 * wn + i;
+                if (tile >= tiles) continue; // wave-uniform: the MFMA below takes operands from every lane
+                const gemm::TileMap tm = gemm::locate<false>(p, tile);
                 const float v[4] = {acc[i][j][0] * scale, acc[i][j][1] * scale, acc[i][j][2] * scale,
                                     acc[i][j][3] * scale};
                 double bs = 0.0;
                 int64_t bi = -1;
-                gemm::lane_epilogue<EPI>(p, tm, q, m, v, bs, bi, p.key_seed, p.key_stream);
+                gemm::LoraProducts lora = {{0.f, 0.f, 0.f, 0.f}, false};
+                if constexpr (EPI == DLK_EPI_QKV) {
+                    const bool vseg = tm.seg == 2;
+                    if (lora_mfma && tm.seg != 1 && (vseg ? p.lora_hidden[2] : p.lora_hidden[0])) {
+                        const uint16_t* up = static_cast<const uint16_t*>(vseg ? p.lora_up[2] : p.lora_up[0]) +
+                                             static_cast<int64_t>(tm.n0 + lane % 16) * p.lora_rank + 8 * (lane_k ? q : 0);
+                        u32x4 raw = *reinterpret_cast<const u32x4*>(up);
+                        if (!lane_k) raw = u32x4{0u, 0u, 0u, 0u};
+                        const bf16x8 a = __builtin_bit_cast(bf16x8, raw);
+                        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, vseg ? hh[1] : hh[0], d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, vseg ? hl[1] : hl[0], d, 0, 0, 0);
+                        lora = {{d[0], d[1], d[2], d[3]}, true};
+                    }
+                }
+                if (m < p.M) gemm::lane_epilogue<EPI>(p, tm, q, m, v, bs, bi, p.key_seed, p.key_stream, lora);
             }
         }
     }

@@ -60,7 +60,8 @@ Kernel resolve_tiles(const dlk_gemv_params& p) {
     }
 }
 
-// Tiled path: prepare_rows splits the activation rows into the staging workspace, then the tiled projection.
+// Tiled path: prepare_rows splits the activation rows into the staging workspace (unless the caller says it
+// already holds them), then the tiled projection.
 int launch_tiles(const dlk_gemv_params& p, hipStream_t stream) {
     using namespace dlk::tiles;
     const Kernel kernel = resolve_tiles(p);
@@ -69,11 +70,12 @@ int launch_tiles(const dlk_gemv_params& p, hipStream_t stream) {
     const bool norm = p.apply_norm && p.epilogue != DLK_EPI_RESIDUAL;
     const void* prep = norm ? reinterpret_cast<const void*>(&prepare_rows<true>)
                             : reinterpret_cast<const void*>(&prepare_rows<false>);
-    hipError_t status = hipLaunchKernel(prep, dim3(p.M), dim3(kPrepThreads), args, 0, stream);
-    if (status != hipSuccess) return static_cast<int>(status);
+    if (!p.stage_ready) {
+        const hipError_t status = hipLaunchKernel(prep, dim3(p.M), dim3(kPrepThreads), args, 0, stream);
+        if (status != hipSuccess) return static_cast<int>(status);
+    }
     const int blocks = col_blocks(p) * row_blocks(p);
-    status = hipLaunchKernel(kernel.fn, dim3(blocks), dim3(kThreads), args, kernel.lds, stream);
-    return static_cast<int>(status);
+    return static_cast<int>(hipLaunchKernel(kernel.fn, dim3(blocks), dim3(kThreads), args, kernel.lds, stream));
 }
 
 int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {

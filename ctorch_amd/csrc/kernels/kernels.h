@@ -89,6 +89,7 @@ typedef struct dlk_gemv_params {
      * batched matrix-core path (64 rows per launch) instead. */
     void* stage;
     int64_t stage_bytes;
+    int stage_ready;        /* the workspace already holds this launch's split rows (same x, norm weight, M, K) */
 } dlk_gemv_params;
 
 /* Floats of workspace that lets dlk_gemv split the keys of this launch (0 when it would not split). */

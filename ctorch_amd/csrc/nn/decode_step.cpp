@@ -84,6 +84,15 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
     const bool kv_bf16 = cache.key().dtype() == DType::bf16;
     const double kv_bytes_per = static_cast<double>(batch) * KV * hd * (kv_bf16 ? 2 : 4);
 
+    // The LoRA down projections and the QKV projection read the same normalised rows: when consecutive launches
+    // take the tiled path with the same staging workspace, the rows are split once.
+    const void* staged = nullptr;
+    auto share_stage = [&](dlk_gemv_params& p) {
+        const bool tiled = p.stage != nullptr && dlk_gemv_stage_bytes(&p) > 0;
+        p.stage_ready = tiled && staged == p.stage ? 1 : 0;
+        staged = tiled ? p.stage : nullptr;
+    };
+
     // 1. LoRA hidden states (down projections of the normalised input), when adapters are attached
     auto lora_down = [&](const nn::LoRAAdapter* adapter, Tensor& hidden) {
         if (!adapter) return;
@@ -99,6 +108,8 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         p.w_bf16 = ab;
         p.y = static_cast<float*>(mutable_data(hidden));
         p.ldy = adapter->rank();
+        ws.attach_workspace(p, device);
+        share_stage(p);
         issue(observer, "lora_down", static_cast<double>(adapter->down().weight().numel()) * (ab ? 2 : 4),
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "LoRA down projection"); });
     };
@@ -153,6 +164,7 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
             throw std::invalid_argument("query and value adapters must share rank and alpha");
         const double bytes = static_cast<double>((H + 2 * KV) * hd * d) * (qb ? 2 : 4) + 2.0 * kv_bytes_per * length;
         ws.attach_workspace(p, device);
+        share_stage(p);
         issue(observer, "qkv_rope_append", bytes,
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "QKV projection"); });
     }
