@@ -34,6 +34,7 @@ GATE_UP_TRAFFIC_BYTES = 46.37e6 + 0.045e6
 C2 = dict(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632)
 C4 = dict(vocab=32000, layers=32, dimensions=4096, heads=32, kv_heads=8, hidden=14336, rope_base=500000.0)
 C5 = dict(C2, lora_rank=16, lora_alpha=32.0)
+C1 = dict(vocab=256, layers=4, dimensions=256, heads=8, kv_heads=2, hidden=688)
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -63,12 +64,13 @@ def parameter_slots(cfg):
     return names
 
 
-def build_model(ct, cfg, context, root=(1234, 0)):
+def build_model(ct, cfg, context, root=(1234, 0), dtype=None):
     """Seeded weights drawn directly in HBM: slot s gets 0.02 * randn(fold_in(root, s)) rounded to bf16 (LoRA up
     matrices 1e-3 * randn); unmerged LoRA adapters on q and v when cfg has lora_rank."""
     gpu = ct.device("gpu")
+    dtype = ct.BF16 if dtype is None else dtype
     decoder = ct.transformer_decoder(cfg["layers"], cfg["dimensions"], cfg["heads"], cfg["kv_heads"], cfg["hidden"],
-                                     context, ct.BF16, gpu, cfg.get("rope_base", 10000.0))
+                                     context, dtype, gpu, cfg.get("rope_base", 10000.0))
     if cfg.get("lora_rank"):
         ct.check(ct.lib().dl_transformer_decoder_attach_lora(decoder.handle, cfg["lora_rank"], cfg["lora_alpha"], 1, 1))
     state, embedding, head = {}, None, None
@@ -76,7 +78,7 @@ def build_model(ct, cfg, context, root=(1234, 0)):
         if name.endswith("norm.weight") or name == "decoder.normalization.weight":
             continue  # RMSNorm weights keep their module default (ones)
         scale = 1e-3 if name.endswith("_adapter.up.weight") else 0.02
-        w = ct.normal(ct.fold_in(root, slot), shape, scale, ct.BF16, gpu)
+        w = ct.normal(ct.fold_in(root, slot), shape, scale, dtype, gpu)
         if name == "tokens.weight":
             embedding = w
         elif name == "output.weight":
@@ -192,6 +194,15 @@ def prefill_c5(ct, decode_steps, batch=4, length=4096):
                 step_bytes=weight_bytes(C5) + kv_bytes(C5, batch, mean_len))
 
 
+def decode_c1(ct, steps=128, prompt_len=32):
+    """C1: the tiny f32 decoder (byte vocabulary), a 32-byte prompt then `steps` greedy steps from the HIP graph
+    (launch-bound: 11 MB of weights sit in the Infinity Cache; reported as an absolute number)."""
+    decoder, lm = build_model(ct, C1, 192, root=(11, 0), dtype=ct.F32)
+    prompt = np.random.default_rng(11).integers(0, C1["vocab"], size=(1, prompt_len), dtype=np.int64)
+    ms, _ = lm.benchmark(prompt, ct.DecoderCache(decoder), 0, steps - 1, 0.0, (0, 0), True)
+    return dict(ms=ms, steps=steps - 1)
+
+
 def cpu_baseline(prompt_len=4, decode_steps=8):
     """The CPU oracle (plain-C restatement of the reference CPU path) on this host, one thread, at the C2 shape:
     a short prompt is fed, then `decode_steps` single-token greedy steps are timed."""
@@ -255,6 +266,10 @@ def main():
                for t in b1["timings"]}
 
     extra = {}
+    c1 = decode_c1(ct)
+    extra["c1"] = {"tok_s": c1["steps"] / (c1["ms"] / 1e3), "us_per_step": 1e3 * c1["ms"] / c1["steps"],
+                   "steps": c1["steps"], "prompt": 32, "dtype": "f32"}
+    log(f"bench: C1 {extra['c1']['us_per_step']:.1f} us/step, {extra['c1']['tok_s']:.0f} tok/s")
     del lm, decoder  # free the C2 model's HBM before the larger workloads
     import gc
     gc.collect()
