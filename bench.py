@@ -187,7 +187,9 @@ def prefill_c5(ct, decode_steps, batch=4, length=4096):
     logits = lm.logits(prompt, cache)
     prefill_ms = timer.stop()
     ids = logits.argmax(-1).reshape(batch, 1).astype(np.int64)
-    ms, _ = lm.benchmark(ids, cache, 2, decode_steps, 0.0, (0, 0), True)
+    ms = 0.0
+    if decode_steps > 0:  # --c5-steps 0: the prefill alone
+        ms, _ = lm.benchmark(ids, cache, 2, decode_steps, 0.0, (0, 0), True)
     flops = prefill_flops(C5, batch, length)
     mean_len = length + 3 + (decode_steps - 1) / 2.0
     return dict(prefill_ms=prefill_ms, flops=flops, decode_ms=ms, batch=batch, length=length,
@@ -300,11 +302,12 @@ def main():
         gc.collect()
         c5 = prefill_c5(ct, args.c5_steps)
         tflops = c5["flops"] / (c5["prefill_ms"] / 1e3) / 1e12
-        ms5 = c5["decode_ms"] / args.c5_steps
+        ms5 = c5["decode_ms"] / max(1, args.c5_steps)
         extra["c5"] = {"prefill_tok_s": c5["batch"] * c5["length"] / (c5["prefill_ms"] / 1e3),
                        "prefill_ms": c5["prefill_ms"], "prefill_TFLOPs": tflops,
                        "mfma_utilisation": tflops / MFMA_BF16_PEAK_TFLOPS, "prefill_flops": c5["flops"],
-                       "decode_tok_s": c5["batch"] * args.c5_steps / (c5["decode_ms"] / 1e3), "decode_ms_per_step": ms5,
+                       "decode_tok_s": c5["batch"] * args.c5_steps / (c5["decode_ms"] / 1e3) if args.c5_steps > 0 else None,
+                       "decode_ms_per_step": ms5 if args.c5_steps > 0 else None,
                        "decode_steps": args.c5_steps, "batch": c5["batch"], "prompt": c5["length"],
                        "lora": "r=16, alpha=32 on q and v (unmerged)"}
         log(f"bench: C5 prefill {c5['prefill_ms']:.1f} ms ({extra['c5']['prefill_tok_s']:.0f} tok/s, "

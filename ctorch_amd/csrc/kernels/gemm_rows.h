@@ -115,13 +115,21 @@ struct LoraProducts {
     bool set;
 };
 
+// QKV: the batch and cache position of activation row m, when the caller computed them once for the row
+// (they take a 64-bit division).
+struct RowPosition {
+    int64_t batch, position;
+    bool set;
+};
+
 // The epilogue of one lane: v[j] = finished dot products of tile rows 4q + j (q = lane / 16) for activation
 // row m of the launch.  QKV: lora (if set) holds the unscaled LoRA products up[n, :] . hidden[m, :] of the
 // same rows, computed by the caller; otherwise they are computed here.
 template <int EPI>
 __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const TileMap& t, int q, int m,
                                               const float (&v)[4], double& best_score, int64_t& best_index,
-                                              uint64_t seed, uint64_t stream, LoraProducts lora = {{}, false}) {
+                                              uint64_t seed, uint64_t stream, LoraProducts lora = {{}, false},
+                                              RowPosition where = {0, 0, false}) {
     using Traits = gemv::WeightTraits<uint16_t>;
     if constexpr (EPI == DLK_EPI_SWIGLU) {
         const int n = t.n0 + 2 * q;
@@ -143,7 +151,8 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
         }
     } else if constexpr (EPI == DLK_EPI_QKV) {
         const int64_t mg = p.m_base + m;
-        const int64_t b = mg / p.length, pos = *p.position + mg % p.length;
+        const int64_t b = where.set ? where.batch : mg / p.length;
+        const int64_t pos = where.set ? where.position : *p.position + mg % p.length;
         const int hd = p.head_dim;
         const float* hidden = t.seg == 0 ? p.lora_hidden[0] : t.seg == 2 ? p.lora_hidden[2] : nullptr;
         const void* lora_up = t.seg == 0 ? p.lora_up[0] : p.lora_up[2];

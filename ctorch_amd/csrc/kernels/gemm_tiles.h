@@ -39,19 +39,28 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kPrepThreads = 256;                  // prepare_rows: one work-group per activation row
 constexpr int kBN = 256;                           // weight rows per work-group (16 tiles of 16)
 constexpr int kBM = 256;                           // activation rows per work-group (16 tiles of 16)
-constexpr int kStages = 3;                         // k steps of 32 in the LDS ring
-constexpr int kWeightBytes = (kBN / 16) * 1024;    // one k step of weight fragments
+constexpr int kActStages = 3;                      // activation ring: k steps of 32
 constexpr int kActBytes = (kBM / 16) * 2048;       // one k step of activation fragments (hi, lo)
-constexpr int kStageBytes = kWeightBytes + kActBytes;
-constexpr size_t kLdsBytes = 0;                    // the ring is static LDS
-constexpr int kDmaPerStep = (kBN / 16 + 2 * (kBM / 16)) / kWaves; // DMA instructions per wave per k step
+constexpr int kWeightPairBytes = (kBN / 16) * 2048; // weight ring: two buffers of one k pair (64) each
+constexpr size_t kLdsBytes = 0;                    // the rings are static LDS
+constexpr int kActDma = 2 * (kBM / 16) / kWaves;   // activation DMA instructions per wave per k step
+constexpr int kWeightDma = 2 * (kBN / 16) / kWaves; // weight DMA instructions per wave per k pair
+static_assert(kActStages * kActBytes + 2 * kWeightPairBytes <= 160 * 1024, "LDS");
 constexpr int kMinBlocks = 64;                     // one row block of 256 takes the tiled path only this wide
 constexpr int kXcds = 8;
-static_assert(kDmaPerStep == 6, "two weight tiles and two activation tiles (hi, lo) per wave");
+static_assert(kActDma == 4 && kWeightDma == 4, "per wave: two activation tiles (hi, lo), two weight tiles (two halves)");
 
-/// Staging workspace of a launch: hi rows, lo rows (bf16 [M][K] each), then the per-row norm factors (f32 [M]).
+/// Staging workspace of a launch: the split rows in fragment order, then the per-row norm factors (f32 [M]).
+/// Fragment order: for each 16-row tile mt (rows up to M rounded to the 256-row block) and 32-wide k step s,
+/// 1 KB of hi then 1 KB of lo, lane l's 16 bytes at 16 l holding row 16 mt + l%16, k 32 s + 8 (l/16) .. +8.  So
+/// every activation DMA reads 1 KB contiguous (consecutive lanes, consecutive 16 bytes: whole 128-byte lines
+/// per 8 lanes, the pattern the global->LDS path serves fastest).
+__host__ __device__ inline int64_t stage_rows(int M) { return (static_cast<int64_t>(M) + 255) / 256 * 256; }
 __host__ __device__ inline int64_t stage_bytes(const dlk_gemv_params& p) {
-    return static_cast<int64_t>(p.M) * p.K * 4 + static_cast<int64_t>(p.M) * 4;
+    return stage_rows(p.M) * p.K * 4 + static_cast<int64_t>(p.M) * 4;
+}
+__host__ __device__ inline const float* stage_inv(const dlk_gemv_params& p) {
+    return reinterpret_cast<const float*>(static_cast<const char*>(p.stage) + stage_rows(p.M) * p.K * 4);
 }
 
 /// Weight-row blocks of a launch: 16 tiles of 16 rows; SwiGLU: 128 features (8 gate tiles + 8 up tiles).
@@ -61,12 +70,21 @@ __host__ __device__ inline int col_blocks(const dlk_gemv_params& p) {
 }
 __host__ __device__ inline int row_blocks(const dlk_gemv_params& p) { return (p.M + kBM - 1) / kBM; }
 
-/// Whether the shape suits the tiled path (host side): bf16 weights, whole k steps, tile-shaped segments, rows
+/// Whether the shape suits the tiled path (host side): bf16 weights, whole k pairs, tile-shaped segments, rows
 /// that prepare_rows reads as float4, and two or more row blocks (or one with a wide weight): narrower launches of
 /// that many rows would take gemm_rows 64 rows at a time, re-streaming the weights and under-filling the device.
 inline bool shape_eligible(const dlk_gemv_params& p) {
-    if (!p.w_bf16 || p.epilogue == DLK_EPI_LOGITS || p.K % 32 != 0 || p.M < kBM) return false;
+    if (!p.w_bf16 || p.epilogue == DLK_EPI_LOGITS || p.K % 64 != 0 || p.M < kBM) return false;
     if (p.ldx % 4 != 0 || reinterpret_cast<uintptr_t>(p.x) % 16 != 0) return false;
+    if ((p.epilogue == DLK_EPI_STORE || p.epilogue == DLK_EPI_RESIDUAL || p.epilogue == DLK_EPI_SWIGLU) &&
+        (p.ldy % 4 != 0 || reinterpret_cast<uintptr_t>(p.y) % 16 != 0)) return false; // 16-byte output stores
+    if (p.epilogue == DLK_EPI_RESIDUAL && (p.ldres % 4 != 0 || reinterpret_cast<uintptr_t>(p.residual) % 16 != 0))
+        return false;
+    if (p.epilogue == DLK_EPI_QKV &&
+        (p.head_dim % 4 != 0 || p.ldy % 4 != 0 || reinterpret_cast<uintptr_t>(p.y) % 16 != 0 ||
+         reinterpret_cast<uintptr_t>(p.cosine) % 8 != 0 || reinterpret_cast<uintptr_t>(p.sine) % 8 != 0 ||
+         reinterpret_cast<uintptr_t>(p.k_cache) % 16 != 0 || reinterpret_cast<uintptr_t>(p.v_cache) % 16 != 0))
+        return false; // vector stores of four head-dim entries
     if (static_cast<int64_t>(kBM) * p.K * 2 >= (int64_t(1) << 31)) return false; // 32-bit DMA lane offsets
     for (int s = 0; s < p.nseg; ++s)
         if (p.seg_rows[s] % gemm::kTile != 0) return false;
@@ -125,19 +143,22 @@ __device__ __forceinline__ const char* tile_base(const dlk_gemv_params& p, int n
     }
 }
 
-// Preparation launch: one work-group per activation row m writes hi[m][k] + lo[m][k] = x[m][k] * g[k] (bf16
-// pair, the remainder rounded once more) and, with the norm, inv[m] = 1/sqrt(mean x^2 + eps) (sum of squares of
-// x in f32).
+// Preparation launch: work-group mt splits the 16-row tile mt.  Wave w takes the k steps s = w, w + 4, ...;
+// lane l (row 16 mt + l % 16, k 32 s + 8 (l / 16) .. +8) writes hi + lo = x * g (bf16 pair, the remainder
+// rounded once more) at 16 l of the step's two 1 KB blocks, so every wave writes whole 1 KB blocks.  With the norm,
+// inv[m] = 1/sqrt(mean x^2 + eps) (sum of squares of x in f32).
 template <bool NORM>
 __global__ __launch_bounds__(kPrepThreads) void prepare_rows(const dlk_gemv_params p) {
-    __shared__ float wave_sums[kPrepThreads / kWave];
-    const int m = blockIdx.x, t = threadIdx.x, K = p.K;
-    const float* x = p.x + static_cast<int64_t>(m) * p.ldx;
-    uint16_t* hi = static_cast<uint16_t*>(p.stage) + static_cast<int64_t>(m) * K;
-    uint16_t* lo = hi + static_cast<int64_t>(p.M) * K;
+    constexpr int kPrepWaves = kPrepThreads / kWave;
+    __shared__ float partial[kPrepWaves][16];
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave, K = p.K, nsteps = K / 32;
+    const int mt = blockIdx.x, r = lane % 16, q = lane / 16;
+    const float* x = p.x + static_cast<int64_t>(min(16 * mt + r, p.M - 1)) * p.ldx; // rows past M repeat the last
+    char* tile = static_cast<char*>(p.stage) + static_cast<int64_t>(mt) * nsteps * 2048 + 16 * lane;
     const bool affine = NORM && p.apply_norm && p.norm_weight;
     float squares = 0.0f;
-    for (int k = 8 * t; k < K; k += 8 * kPrepThreads) {
+    for (int s = wave; s < nsteps; s += kPrepWaves) {
+        const int k = 32 * s + 8 * q;
         const float4 a = *reinterpret_cast<const float4*>(x + k);
         const float4 b = *reinterpret_cast<const float4*>(x + k + 4);
         f32x8 v = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -147,9 +168,9 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_rows(const dlk_gemv_para
             if (affine) {
                 f32x8 g;
                 if (p.norm_bf16) {
-                    const u32x4 r = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.norm_weight) + k);
-                    g = f32x8{bf16_lo(r.x), bf16_hi(r.x), bf16_lo(r.y), bf16_hi(r.y),
-                              bf16_lo(r.z), bf16_hi(r.z), bf16_lo(r.w), bf16_hi(r.w)};
+                    const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p.norm_weight) + k);
+                    g = f32x8{bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y),
+                              bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
                 } else {
                     const float4 g0 = *reinterpret_cast<const float4*>(static_cast<const float*>(p.norm_weight) + k);
                     const float4 g1 =
@@ -161,21 +182,22 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_rows(const dlk_gemv_para
         }
         const bf16x8 h = __builtin_convertvector(v, bf16x8);
         const bf16x8 l = __builtin_convertvector(v - __builtin_convertvector(h, f32x8), bf16x8);
-        *reinterpret_cast<bf16x8*>(hi + k) = h;
-        *reinterpret_cast<bf16x8*>(lo + k) = l;
+        *reinterpret_cast<bf16x8*>(tile + static_cast<int64_t>(s) * 2048) = h;
+        *reinterpret_cast<bf16x8*>(tile + static_cast<int64_t>(s) * 2048 + 1024) = l;
     }
     if constexpr (NORM) {
         if (p.apply_norm) {
-            squares = wave_sum(squares);
-            if (t % kWave == 0) wave_sums[t / kWave] = squares;
+            // lanes r, r + 16, r + 32, r + 48 hold the four k quarters of row r; then the waves through LDS
+            squares += __shfl_xor(squares, 16, kWave);
+            squares += __shfl_xor(squares, 32, kWave);
+            if (q == 0) partial[wave][r] = squares;
             gemv::lds_barrier();
-            if (t == 0) {
+            const int m = 16 * mt + t;
+            if (t < 16 && m < p.M) {
                 float total = 0.0f;
 #pragma unroll
-                for (int w = 0; w < kPrepThreads / kWave; ++w) total += wave_sums[w];
-                float* inv =
-                    reinterpret_cast<float*>(static_cast<uint16_t*>(p.stage) + 2 * static_cast<int64_t>(p.M) * K);
-                inv[m] = rsqrtf(total / static_cast<float>(K) + p.epsilon);
+                for (int w = 0; w < kPrepWaves; ++w) total += partial[w][t];
+                const_cast<float*>(stage_inv(p))[m] = rsqrtf(total / static_cast<float>(K) + p.epsilon);
             }
         }
     }
@@ -184,7 +206,8 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_rows(const dlk_gemv_para
 template <int EPI, bool NORM>
 __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params p) {
     constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
-    __shared__ __attribute__((aligned(1024))) char ring[kStages][kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char wring[2][kWeightPairBytes];
+    __shared__ __attribute__((aligned(1024))) char xring[kActStages][kActBytes];
 
     const int t = threadIdx.x, lane = t % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
@@ -192,40 +215,49 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
     const int tiles = gemm::tiles_of(p);
     const int nb = col_blocks(p), total = nb * row_blocks(p);
 
-    // XCD-aware placement: XCD x runs logical tiles [start_x, start_x + count_x)
+    // XCD-aware placement: XCD x runs logical tiles [start_x, start_x + count_x) (a sweep of 2 x 32 grouping
+    // shapes for the work-groups one XCD runs at once changed nothing measurable)
     const int per = total / kXcds, rem = total % kXcds;
     const int xcd = blockIdx.x % kXcds, idx = blockIdx.x / kXcds;
     const int logical = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
     const int n_blk = logical % nb, m_blk = logical / nb;
     const int m_first = m_blk * kBM;
 
-    // DMA sources: a wave-uniform base per instruction and a 32-bit lane offset; lane i loads row i%16 at k
-    // 8 (i/16).  Wave w fills weight tiles 2w, 2w+1 and activation tiles 2w, 2w+1 (hi and lo); activation
-    // rows past M re-read row M-1 (their results are never stored).
+    // Weights: a 64-wide k pair of a 16-row tile is 2 KB of LDS, two halves of 8 rows x 128 bytes; each DMA
+    // instruction reads 8 whole 128-byte lines (8 lanes per row), which the global->LDS path serves ~3.7x faster
+    // than 16 half lines.  Row R of the tile keeps its 16-byte column g at slot g ^ (R >> 1) (XOR swizzle), so
+    // the 16 lanes of an MFMA fragment read (rows 0..15, one column) hit 16 different bank groups.  Wave w fills
+    // tiles 2w, 2w+1 (both halves).
     const char* wbase[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) wbase[j] = tile_base<SWIGLU>(p, n_blk, 2 * wave + j, tiles);
-    const uint32_t woff = static_cast<uint32_t>(lane % 16) * K * 2 + 16 * (lane / 16);
-    const uint16_t* const shi = static_cast<const uint16_t*>(p.stage);
-    const int64_t lo_delta = static_cast<int64_t>(p.M) * K * 2; // bytes from the hi rows to the lo rows
-    const char* xbase[2];
-    uint32_t xoff[2];
+    uint32_t woff[2]; // per half h: lane i -> row 8 h + i / 8, slot i % 8 <- column (i % 8) ^ ((8 h + i / 8) >> 1)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int first = min(m_first + 16 * (2 * wave + h), p.M - 1);
-        const int row = min(m_first + 16 * (2 * wave + h) + lane % 16, p.M - 1);
-        xbase[h] = reinterpret_cast<const char*>(shi + static_cast<int64_t>(first) * K);
-        xoff[h] = static_cast<uint32_t>(row - first) * K * 2 + 16 * (lane / 16);
+        const int R = 8 * h + lane / 8;
+        woff[h] = static_cast<uint32_t>(R) * K * 2 + 16 * ((lane % 8) ^ (R >> 1));
     }
-    auto issue = [&](int step, char* buf) {
+    // activation tiles in the staging workspace's fragment order: (tile, step) is 2 KB (hi, lo) at
+    // ((tile * nsteps) + step) * 2048 (rows past M hold whatever was there: their results are never stored)
+    const char* xbase[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        xbase[h] = static_cast<const char*>(p.stage) + static_cast<int64_t>(m_first / 16 + 2 * wave + h) * nsteps * 2048;
+    const uint32_t xoff = 16 * lane;
+    auto issue_weights = [&](int pair, char* buf) {
         const uint32_t b = lds_offset(buf);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) dma16(wbase[j] + 64 * step, woff, b + (2 * wave + j) * 1024);
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) dma16(wbase[j] + 128 * pair, woff[h], b + (2 * wave + j) * 2048 + h * 1024);
+    };
+    auto issue_acts = [&](int step, char* buf) {
+        const uint32_t b = lds_offset(buf);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint32_t dst = b + kWeightBytes + (2 * wave + h) * 2048;
-            dma16(xbase[h] + 64 * step, xoff[h], dst);
-            dma16(xbase[h] + lo_delta + 64 * step, xoff[h], dst + 1024);
+            const uint32_t dst = b + (2 * wave + h) * 2048;
+            dma16(xbase[h] + 2048 * step, xoff, dst);
+            dma16(xbase[h] + 2048 * step + 1024, xoff, dst + 1024);
         }
     };
 
@@ -239,11 +271,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](const char* base) {
+    // weight fragment of k step s' (0, 1) of the pair: row R = lane % 16, column 4 s' + lane / 16, swizzled
+    const int R = lane % 16;
+    uint32_t wfrag[2];
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) wfrag[sp] = (R / 8) * 1024 + (R % 8) * 128 + 16 * ((4 * sp + lane / 16) ^ (R >> 1));
+    auto compute = [&](const char* wbuf, int sp, const char* xbuf) {
         bf16x8 bh[4], bl[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const char* frag = base + kWeightBytes + (4 * wm + j) * 2048 + 16 * lane;
+            const char* frag = xbuf + (4 * wm + j) * 2048 + 16 * lane;
             bh[j] = *reinterpret_cast<const bf16x8*>(frag);
             bl[j] = *reinterpret_cast<const bf16x8*>(frag + 1024);
         }
@@ -251,7 +288,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
         for (int i = 0; i < 8; ++i) {
             // weight tiles past the end (a narrow launch) hold repeats of the last tile: no products for them
             if (!SWIGLU && 16 * n_blk + slot_tile(i) >= tiles) continue;
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(base + slot_tile(i) * 1024 + 16 * lane);
+            const bf16x8 a = *reinterpret_cast<const bf16x8*>(wbuf + slot_tile(i) * 2048 + wfrag[sp]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh[j], acc[i][j], 0, 0, 0);
@@ -260,26 +297,40 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
         }
     };
 
-    // Ring of kStages buffers.  Before step c's barrier every wave waits for its own DMA of step c (steps c+1 ..
-    // c+kStages-2 stay in flight); the barrier then makes every wave's step-c data visible and tells that step
-    // c-1's buffer is no longer read, so step c+kStages-1 is issued into it.  Past the last step the issue
-    // repeats the last step into that unread buffer, keeping the in-flight count uniform.
-#pragma unroll
-    for (int s = 0; s < kStages - 1; ++s) issue(min(s, nsteps - 1), ring[s]);
-    int buf = 0;
-    for (int c = 0; c < nsteps; ++c) {
-        wait_vm<(kStages - 2) * kDmaPerStep>();
+    // Two rings.  Activations: three buffers of one k step; weights: two buffers of one k pair.  Step j issues,
+    // after its barrier, the weights of pair j/2 + 1 (even j only: its buffer held pair j/2 - 1, which every wave
+    // finished before this barrier) and the activations of step j + 2 (into the buffer of step j - 1).  Before
+    // step c's barrier a wave waits until only step c-1's DMAs are in flight (8 after an even step, 4 after an
+    // odd one), so its own DMAs of step c's data are done; the barrier makes every wave's visible.  Issues past
+    // the end repeat the last pair or step into a buffer nobody reads again, keeping the counts uniform.  The
+    // prologue issues what steps -2 and -1 would.  nsteps is even.
+    const int npairs = nsteps / 2;
+    issue_weights(0, wring[0]);
+    issue_acts(0, xring[0]);
+    issue_acts(min(1, nsteps - 1), xring[1]);
+    int xb = 0;
+    for (int c = 0; c < nsteps; c += 2) {
+        const int pair = c / 2;
+        // even step c: weights pair `pair` (first half of its k), activations of step c
+        wait_vm<kActDma>();
         ring_barrier();
-        issue(min(c + kStages - 1, nsteps - 1), ring[buf == 0 ? kStages - 1 : buf - 1]);
-        compute(ring[buf]);
-        buf = buf + 1 == kStages ? 0 : buf + 1;
+        issue_weights(min(pair + 1, npairs - 1), wring[(pair + 1) & 1]);
+        issue_acts(min(c + 2, nsteps - 1), xring[xb == 0 ? kActStages - 1 : xb - 1]);
+        compute(wring[pair & 1], 0, xring[xb]);
+        xb = xb + 1 == kActStages ? 0 : xb + 1;
+        // odd step c + 1
+        wait_vm<kActDma + kWeightDma>();
+        ring_barrier();
+        issue_acts(min(c + 3, nsteps - 1), xring[xb == 0 ? kActStages - 1 : xb - 1]);
+        compute(wring[pair & 1], 1, xring[xb]);
+        xb = xb + 1 == kActStages ? 0 : xb + 1;
     }
     wait_vm<0>();
 
     const bool norm = NORM && p.apply_norm;
     float inv[4] = {1.f, 1.f, 1.f, 1.f};
     if (norm) {
-        const float* row_inv = reinterpret_cast<const float*>(shi + 2 * static_cast<int64_t>(p.M) * K);
+        const float* row_inv = stage_inv(p);
 #pragma unroll
         for (int j = 0; j < 4; ++j) inv[j] = row_inv[min(m_first + 64 * wm + 16 * j + lane % 16, p.M - 1)];
     }
@@ -296,9 +347,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
                 const int m = m_first + 64 * wm + 16 * j + lane % 16;
                 if (m >= p.M) continue;
                 const float scale = inv[j] * p.acc_scale;
-                float* dst = p.y + static_cast<int64_t>(m) * p.ldy + f;
+                float o[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) dst[r] = gemv::silu(acc[i][j][r] * scale) * (acc[i + 4][j][r] * scale);
+                for (int r = 0; r < 4; ++r) o[r] = gemv::silu(acc[i][j][r] * scale) * (acc[i + 4][j][r] * scale);
+                *reinterpret_cast<float4*>(p.y + static_cast<int64_t>(m) * p.ldy + f) = make_float4(o[0], o[1], o[2], o[3]);
             }
         }
     } else {
@@ -308,10 +360,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
         const bool lora_mfma = EPI == DLK_EPI_QKV && p.lora_rank > 0 && p.lora_rank <= 32 && p.lora_rank % 8 == 0;
         const bool lane_k = 8 * q < p.lora_rank; // lanes whose k slots hold rank entries
         // fully unrolled: acc is only ever indexed with constants (a runtime index puts it in scratch memory)
+        const int64_t first_pos = EPI == DLK_EPI_QKV ? *p.position : 0;
 #pragma clang loop unroll(full)
         for (int j = 0; j < 4; ++j) {
             const int ml = 64 * wm + 16 * j + lane % 16, m = m_first + ml;
             const float scale = inv[j] * p.acc_scale;
+            gemm::RowPosition where = {0, 0, false};
+            if constexpr (EPI == DLK_EPI_QKV) {
+                const int64_t mg = p.m_base + m;
+                where = {mg / p.length, first_pos + mg % p.length, true};
+            }
             // hidden fragments of segments 0 (q) and 2 (v); the kernel-argument arrays and these are only indexed
             // with constants or selects (a runtime index would copy them to scratch memory)
             bf16x8 hh[2] = {}, hl[2] = {};
@@ -355,7 +413,56 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
                         lora = {{d[0], d[1], d[2], d[3]}, true};
                     }
                 }
-                if (m < p.M) gemm::lane_epilogue<EPI>(p, tm, q, m, v, bs, bi, p.key_seed, p.key_stream, lora);
+                if (m >= p.M) continue;
+                if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL) {
+                    if (EPI == DLK_EPI_RESIDUAL || !p.bias) {
+                        // four consecutive outputs of row m: one 16-byte store (and residual load)
+                        const int n = tm.n0 + 4 * q;
+                        float4 out = make_float4(v[0], v[1], v[2], v[3]);
+                        if constexpr (EPI == DLK_EPI_RESIDUAL) {
+                            const float4 r = *reinterpret_cast<const float4*>(p.residual + static_cast<int64_t>(m) * p.ldres + n);
+                            out.x += r.x; out.y += r.y; out.z += r.z; out.w += r.w;
+                        }
+                        *reinterpret_cast<float4*>(p.y + static_cast<int64_t>(m) * p.ldy + n) = out;
+                        continue;
+                    }
+                }
+                if constexpr (EPI == DLK_EPI_QKV) {
+                    // four consecutive head-dim entries d .. d+3 of one head: LoRA, RoPE on the pairs (d, d+1),
+                    // (d+2, d+3) (interleaved, src/ops/contraction.cpp:44-49), then one 16-byte q store or one
+                    // 8-byte (bf16) / 16-byte (f32) K or V cache store
+                    const int n = tm.n0 + 4 * q, hd = p.head_dim, d = n % hd, head = n / hd;
+                    float o[4] = {v[0], v[1], v[2], v[3]};
+                    if (lora.set) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[r] += lora.v[r] * p.lora_scale;
+                    } else if (tm.seg != 1 && (tm.seg == 0 ? p.lora_hidden[0] : p.lora_hidden[2])) {
+                        gemm::lane_epilogue<EPI>(p, tm, q, m, v, bs, bi, p.key_seed, p.key_stream, lora, where);
+                        continue; // ranks the MFMA pair does not take: the scalar path
+                    }
+                    if (tm.seg < 2) {
+                        const int64_t table = where.position * (hd / 2) + d / 2;
+                        const float2 c = *reinterpret_cast<const float2*>(p.cosine + table);
+                        const float2 sn = *reinterpret_cast<const float2*>(p.sine + table);
+                        const float e0 = o[0] * c.x - o[1] * sn.x, o0 = o[0] * sn.x + o[1] * c.x;
+                        const float e1 = o[2] * c.y - o[3] * sn.y, o1 = o[2] * sn.y + o[3] * c.y;
+                        o[0] = e0; o[1] = o0; o[2] = e1; o[3] = o1;
+                    }
+                    if (tm.seg == 0) {
+                        *reinterpret_cast<float4*>(p.y + (p.m_base + m) * p.ldy + n) = make_float4(o[0], o[1], o[2], o[3]);
+                    } else {
+                        const int64_t index = ((where.batch * p.kv_heads + head) * p.cache_capacity + where.position) * hd + d;
+                        void* cache = tm.seg == 1 ? p.k_cache : p.v_cache;
+                        if (p.cache_bf16)
+                            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(cache) + index) =
+                                make_uint2(f32_to_bf16(o[0]) | (static_cast<uint32_t>(f32_to_bf16(o[1])) << 16),
+                                           f32_to_bf16(o[2]) | (static_cast<uint32_t>(f32_to_bf16(o[3])) << 16));
+                        else
+                            *reinterpret_cast<float4*>(static_cast<float*>(cache) + index) = make_float4(o[0], o[1], o[2], o[3]);
+                    }
+                    continue;
+                }
+                gemm::lane_epilogue<EPI>(p, tm, q, m, v, bs, bi, p.key_seed, p.key_stream, lora, where);
             }
         }
     }

@@ -71,7 +71,7 @@ int launch_tiles(const dlk_gemv_params& p, hipStream_t stream) {
     const void* prep = norm ? reinterpret_cast<const void*>(&prepare_rows<true>)
                             : reinterpret_cast<const void*>(&prepare_rows<false>);
     if (!p.stage_ready) {
-        const hipError_t status = hipLaunchKernel(prep, dim3(p.M), dim3(kPrepThreads), args, 0, stream);
+        const hipError_t status = hipLaunchKernel(prep, dim3((p.M + 15) / 16), dim3(kPrepThreads), args, 0, stream);
         if (status != hipSuccess) return static_cast<int>(status);
     }
     const int blocks = col_blocks(p) * row_blocks(p);
