@@ -36,7 +36,8 @@ using gemv::u32x4;
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 constexpr int kThreads = 512;                      // 8 waves
 constexpr int kWaves = kThreads / kWave;
-constexpr int kPrepThreads = 256;                  // prepare_rows: one work-group per activation row
+constexpr int kPrepThreads = 256;                  // prepare_rows: one work-group per 16-row tile and k chunk
+constexpr int kPrepChunk = 512;                    // k per prepare_rows work-group
 constexpr int kBN = 256;                           // weight rows per work-group (16 tiles of 16)
 constexpr int kBM = 256;                           // activation rows per work-group (16 tiles of 16)
 constexpr int kActStages = 3;                      // activation ring: k steps of 32
@@ -50,17 +51,27 @@ constexpr int kMinBlocks = 64;                     // one row block of 256 takes
 constexpr int kXcds = 8;
 static_assert(kActDma == 4 && kWeightDma == 4, "per wave: two activation tiles (hi, lo), two weight tiles (two halves)");
 
-/// Staging workspace of a launch: the split rows in fragment order, then the per-row norm factors (f32 [M]).
+/// Staging workspace of a launch: the split rows in fragment order, then per-k-chunk sums of squares of each row
+/// (f32 [ceil(K / 512)][M]; the norm factor of row m is 1/sqrt(sum over chunks / K + eps), summed in chunk order).
 /// Fragment order: for each 16-row tile mt (rows up to M rounded to the 256-row block) and 32-wide k step s,
 /// 1 KB of hi then 1 KB of lo, lane l's 16 bytes at 16 l holding row 16 mt + l%16, k 32 s + 8 (l/16) .. +8.  So
 /// every activation DMA reads 1 KB contiguous (consecutive lanes, consecutive 16 bytes: whole 128-byte lines
 /// per 8 lanes, the pattern the global->LDS path serves fastest).
 __host__ __device__ inline int64_t stage_rows(int M) { return (static_cast<int64_t>(M) + 255) / 256 * 256; }
+__host__ __device__ inline int prep_chunks(int K) { return (K + kPrepChunk - 1) / kPrepChunk; }
 __host__ __device__ inline int64_t stage_bytes(const dlk_gemv_params& p) {
-    return stage_rows(p.M) * p.K * 4 + static_cast<int64_t>(p.M) * 4;
+    return stage_rows(p.M) * p.K * 4 + static_cast<int64_t>(prep_chunks(p.K)) * p.M * 4;
 }
-__host__ __device__ inline const float* stage_inv(const dlk_gemv_params& p) {
+__host__ __device__ inline const float* stage_squares(const dlk_gemv_params& p) {
     return reinterpret_cast<const float*>(static_cast<const char*>(p.stage) + stage_rows(p.M) * p.K * 4);
+}
+/// Norm factor of row m (0 <= m < M) from the chunk sums, in chunk order.
+__device__ __forceinline__ float stage_inv(const dlk_gemv_params& p, int m) {
+    const float* sq = stage_squares(p);
+    const int chunks = prep_chunks(p.K);
+    float total = 0.0f;
+    for (int c = 0; c < chunks; ++c) total += sq[static_cast<int64_t>(c) * p.M + m];
+    return rsqrtf(total / static_cast<float>(p.K) + p.epsilon);
 }
 
 /// Weight-row blocks of a launch: 16 tiles of 16 rows; SwiGLU: 128 features (8 gate tiles + 8 up tiles).
@@ -143,21 +154,22 @@ __device__ __forceinline__ const char* tile_base(const dlk_gemv_params& p, int n
     }
 }
 
-// Preparation launch: work-group mt splits the 16-row tile mt.  Wave w takes the k steps s = w, w + 4, ...;
-// lane l (row 16 mt + l % 16, k 32 s + 8 (l / 16) .. +8) writes hi + lo = x * g (bf16 pair, the remainder
-// rounded once more) at 16 l of the step's two 1 KB blocks, so every wave writes whole 1 KB blocks.  With the norm,
-// inv[m] = 1/sqrt(mean x^2 + eps) (sum of squares of x in f32).
+// Preparation launch: work-group (mt, c) splits rows 16 mt .. +16 over k chunk c (512 wide).  Wave w takes the
+// chunk's k steps w, w + 4, ...; lane l (row 16 mt + l % 16, k 32 s + 8 (l / 16) .. +8) writes hi + lo = x * g
+// (bf16 pair, the remainder rounded once more) at 16 l of the step's two 1 KB blocks, so every wave writes whole
+// 1 KB blocks.  With the norm the work-group writes the chunk's sum of squares of x (f32) for each row.
 template <bool NORM>
 __global__ __launch_bounds__(kPrepThreads) void prepare_rows(const dlk_gemv_params p) {
     constexpr int kPrepWaves = kPrepThreads / kWave;
     __shared__ float partial[kPrepWaves][16];
     const int t = threadIdx.x, lane = t % kWave, wave = t / kWave, K = p.K, nsteps = K / 32;
-    const int mt = blockIdx.x, r = lane % 16, q = lane / 16;
+    const int mt = blockIdx.x, chunk = blockIdx.y, r = lane % 16, q = lane / 16;
     const float* x = p.x + static_cast<int64_t>(min(16 * mt + r, p.M - 1)) * p.ldx; // rows past M repeat the last
     char* tile = static_cast<char*>(p.stage) + static_cast<int64_t>(mt) * nsteps * 2048 + 16 * lane;
     const bool affine = NORM && p.apply_norm && p.norm_weight;
+    const int s_end = min(nsteps, (chunk + 1) * (kPrepChunk / 32));
     float squares = 0.0f;
-    for (int s = wave; s < nsteps; s += kPrepWaves) {
+    for (int s = chunk * (kPrepChunk / 32) + wave; s < s_end; s += kPrepWaves) {
         const int k = 32 * s + 8 * q;
         const float4 a = *reinterpret_cast<const float4*>(x + k);
         const float4 b = *reinterpret_cast<const float4*>(x + k + 4);
@@ -187,7 +199,7 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_rows(const dlk_gemv_para
     }
     if constexpr (NORM) {
         if (p.apply_norm) {
-            // lanes r, r + 16, r + 32, r + 48 hold the four k quarters of row r; then the waves through LDS
+            // lanes r, r + 16, r + 32, r + 48 hold four k quarters of row r; then the waves through LDS
             squares += __shfl_xor(squares, 16, kWave);
             squares += __shfl_xor(squares, 32, kWave);
             if (q == 0) partial[wave][r] = squares;
@@ -197,7 +209,7 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_rows(const dlk_gemv_para
                 float total = 0.0f;
 #pragma unroll
                 for (int w = 0; w < kPrepWaves; ++w) total += partial[w][t];
-                const_cast<float*>(stage_inv(p))[m] = rsqrtf(total / static_cast<float>(K) + p.epsilon);
+                const_cast<float*>(stage_squares(p))[static_cast<int64_t>(chunk) * p.M + m] = total;
             }
         }
     }
@@ -330,9 +342,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
     const bool norm = NORM && p.apply_norm;
     float inv[4] = {1.f, 1.f, 1.f, 1.f};
     if (norm) {
-        const float* row_inv = stage_inv(p);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) inv[j] = row_inv[min(m_first + 64 * wm + 16 * j + lane % 16, p.M - 1)];
+        for (int j = 0; j < 4; ++j) inv[j] = stage_inv(p, min(m_first + 64 * wm + 16 * j + lane % 16, p.M - 1));
     }
 
     const int q = lane / 16;

@@ -60,22 +60,30 @@ Kernel resolve_tiles(const dlk_gemv_params& p) {
     }
 }
 
+int launch_prepare(const dlk_gemv_params& p, hipStream_t stream);
+
 // Tiled path: prepare_rows splits the activation rows into the staging workspace (unless the caller says it
 // already holds them), then the tiled projection.
 int launch_tiles(const dlk_gemv_params& p, hipStream_t stream) {
     using namespace dlk::tiles;
     const Kernel kernel = resolve_tiles(p);
     if (!kernel.fn) return static_cast<int>(hipErrorInvalidValue);
+    const int status = launch_prepare(p, stream);
+    if (status != 0) return status;
+    void* args[] = {const_cast<dlk_gemv_params*>(&p)};
+    const int blocks = col_blocks(p) * row_blocks(p);
+    return static_cast<int>(hipLaunchKernel(kernel.fn, dim3(blocks), dim3(kThreads), args, kernel.lds, stream));
+}
+
+int launch_prepare(const dlk_gemv_params& p, hipStream_t stream) {
+    using namespace dlk::tiles;
+    if (p.stage_ready) return 0;
     void* args[] = {const_cast<dlk_gemv_params*>(&p)};
     const bool norm = p.apply_norm && p.epilogue != DLK_EPI_RESIDUAL;
     const void* prep = norm ? reinterpret_cast<const void*>(&prepare_rows<true>)
                             : reinterpret_cast<const void*>(&prepare_rows<false>);
-    if (!p.stage_ready) {
-        const hipError_t status = hipLaunchKernel(prep, dim3((p.M + 15) / 16), dim3(kPrepThreads), args, 0, stream);
-        if (status != hipSuccess) return static_cast<int>(status);
-    }
-    const int blocks = col_blocks(p) * row_blocks(p);
-    return static_cast<int>(hipLaunchKernel(kernel.fn, dim3(blocks), dim3(kThreads), args, kernel.lds, stream));
+    return static_cast<int>(
+        hipLaunchKernel(prep, dim3((p.M + 15) / 16, prep_chunks(p.K)), dim3(kPrepThreads), args, 0, stream));
 }
 
 int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
@@ -153,7 +161,8 @@ int launch_waves(const dlk_gemv_params& p) {
 } // namespace
 
 extern "C" int64_t dlk_gemv_split_floats(const dlk_gemv_params* p) {
-    if (dlk::tiles::eligible(*p) || !dlk::gemm::eligible(*p)) return 0;
+    if (dlk::tiles::eligible(*p)) return 0;
+    if (!dlk::gemm::eligible(*p)) return 0;
     const int rows = std::min(p->M, dlk::gemm::kMaxRows);
     return dlk::gemm::split_floats(*p, dlk::gemm::splits_of(*p, rows), rows);
 }
