@@ -41,6 +41,27 @@ __device__ __forceinline__ void split8(const f32x8 v, bf16x8& hi, bf16x8& lo) {
     lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x8), bf16x8);
 }
 
+// The same split with the hi values widened back from the packed pairs (low half: << 16, high half: mask), one
+// conversion per pair instead of one per value.
+__device__ __forceinline__ void split8_pairs(const f32x8 v, bf16x8& hi, bf16x8& lo) {
+    const u32x4 h = __builtin_bit_cast(u32x4, __builtin_convertvector(v, bf16x8));
+    const f32x8 back = {__uint_as_float(h.x << 16), __uint_as_float(h.x & 0xffff0000u),
+                        __uint_as_float(h.y << 16), __uint_as_float(h.y & 0xffff0000u),
+                        __uint_as_float(h.z << 16), __uint_as_float(h.z & 0xffff0000u),
+                        __uint_as_float(h.w << 16), __uint_as_float(h.w & 0xffff0000u)};
+    hi = __builtin_bit_cast(bf16x8, h);
+    lo = __builtin_convertvector(v - back, bf16x8);
+}
+
+// Maximum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the lanes that hold one query row): the lane-swap
+// instructions exchange the two wave halves, then adjacent 16-lane rows, in registers.
+__device__ __forceinline__ float max_over_rows(float x) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ void block_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
@@ -143,12 +164,17 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
         }
     };
 
-    f32x4 o[2][DT];
-    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    // o: the output accumulators; l: the running row sums, taken by the matrix cores as a ones row of V^T times
+    // P^T (every entry of l[qt] holds the sum of the lane's query row, so no cross-lane step is needed)
+    f32x4 o[2][DT], l[2];
+    float m_run[2] = {-INFINITY, -INFINITY};
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int qt = 0; qt < 2; ++qt) {
+        l[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int d = 0; d < DT; ++d) o[qt][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
 
     // one key tile; MASK: the tile crosses the causal diagonal of some row of the work-group
     auto step = [&](int tile, auto mask_tag) {
@@ -157,19 +183,30 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
         if (tile + 1 < tiles) load(tile + 1);
 
         // scores: s[i][qt] = S[keys 64 tile + 16 i + 4 q + j][query row (qt, lane % 16)]
+        // the K fragments are read ahead so that the reads overlap: the whole tile at head dim 64, one 16-key
+        // block at a time at 128 (whose registers would not hold the whole tile)
+        bf16x8 kf[4][KS];
+        auto read_k = [&](int i) {
+#pragma unroll
+            for (int st = 0; st < KS; ++st)
+                kf[i][st] = *reinterpret_cast<const bf16x8*>(&ks[buf][(16 * i + lane % 16) * KSTRIDE + 32 * st + 8 * q]);
+        };
+        if constexpr (HD == 64) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) read_k(i);
+        }
         f32x4 s[4][2];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            if constexpr (HD != 64) read_k(i);
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) s[i][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int st = 0; st < KS; ++st) {
-                const bf16x8 a =
-                    *reinterpret_cast<const bf16x8*>(&ks[buf][(16 * i + lane % 16) * KSTRIDE + 32 * st + 8 * q]);
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) {
-                    s[i][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qh[qt][st], s[i][qt], 0, 0, 0);
-                    s[i][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ql[qt][st], s[i][qt], 0, 0, 0);
+                    s[i][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i][st], qh[qt][st], s[i][qt], 0, 0, 0);
+                    s[i][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i][st], ql[qt][st], s[i][qt], 0, 0, 0);
                 }
             }
         }
@@ -190,36 +227,35 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
                     }
                     mx = fmaxf(mx, v);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            mx = max_over_rows(mx);
             // key 0 is visible to every row, so m_new is finite from the first tile on; exp2(-inf) = 0
             const float m_new = fmaxf(m_run[qt], mx);
             const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
-            float sum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float e = __builtin_amdgcn_exp2f(s[i][qt][j] - m_new);
-                    s[i][qt][j] = e;
-                    sum += e;
-                }
-            sum += __shfl_xor(sum, 16, kWave);
-            sum += __shfl_xor(sum, 32, kWave);
-            l_run[qt] = l_run[qt] * alpha + sum;
+                for (int j = 0; j < 4; ++j) s[i][qt][j] = __builtin_amdgcn_exp2f(s[i][qt][j] - m_new);
             m_run[qt] = m_new;
             if (!__all(alpha == 1.0f)) { // the running maxima of the wave's rows moved
+                l[qt] *= alpha;
 #pragma unroll
                 for (int d = 0; d < DT; ++d) o[qt][d] *= alpha;
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u)
-                split8(f32x8{s[2 * u][qt][0], s[2 * u][qt][1], s[2 * u][qt][2], s[2 * u][qt][3],
+                split8_pairs(f32x8{s[2 * u][qt][0], s[2 * u][qt][1], s[2 * u][qt][2], s[2 * u][qt][3],
                              s[2 * u + 1][qt][0], s[2 * u + 1][qt][1], s[2 * u + 1][qt][2], s[2 * u + 1][qt][3]},
                        ph[u][qt], pl[u][qt]);
         }
 
         // O^T += V^T P^T: lane (d = 16 dt + lane % 16, q) supplies V[keys 32 u + 4 q .. +4, 32 u + 16 + 4 q .. +4][d]
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, ph[u][qt], l[qt], 0, 0, 0);
+                l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pl[u][qt], l[qt], 0, 0, 0);
+            }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
@@ -249,7 +285,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         if (!valid[qt]) continue;
-        const float inv = 1.0f / l_run[qt];
+        const float inv = 1.0f / l[qt][0];
         float* out = p.out + (static_cast<int64_t>(b) * p.L + pos[qt]) * p.ldo + static_cast<int64_t>(head[qt]) * HD;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
