@@ -11,14 +11,16 @@
 //   S^T[16 keys][16 queries] = K[16][HD] * Q[16][HD]^T   (v_mfma_f32_16x16x32_bf16; A = K rows from LDS,
 //                                                         B = the query rows, split into bf16 hi + lo)
 // so lane l holds S[keys 4(l/16) .. +4][query l%16]: the online softmax of query l%16 runs on the lane's own
-// values plus two cross-lane steps, and the probabilities of two adjacent 16-key tiles are already the B
+// values plus one cross-lane maximum, and the probabilities of two adjacent 16-key tiles are already the B
 // operand of
 //   O^T[16 d][16 queries] += V^T[16 d][32 keys] * P^T     (A = V^T from the transposed LDS tile, in the key
 //                                                         order the lane holds; P split into hi + lo)
 // Two MFMAs per product (hi and lo) keep f32-level accuracy against the bf16 K and V.  The softmax runs in base 2
 // (log2 e folded into the score scale, one v_exp_f32 per score) and masks only the tiles that cross the causal
-// diagonal.  Keys at or past the end of the sequence are staged as zeros, so stale cache rows never reach the
-// products.
+// diagonal.  The row maxima cross the four lanes of a row with the in-register lane swaps (v_permlane32_swap,
+// v_permlane16_swap); the row sums come out of the matrix cores as one more output tile whose A operand is all
+// ones, so every lane holds its row's sum with no cross-lane step.  Keys at or past the end of the sequence are
+// staged as zeros, so stale cache rows never reach the products.
 #include "kernels/device_common.h"
 
 #include <type_traits>
