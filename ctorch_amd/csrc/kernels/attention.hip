@@ -474,6 +474,251 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
     }
 }
 
+// ------------------------------------------------------------------------------------------ streaming decode
+// One new position per sequence (L = 1) over bf16 K/V, HD 64 or 128, G = H/KV <= 4.  A work-group of four
+// waves takes one (sequence, KV head, key chunk); each wave streams its own run of chunk / 4 keys in tiles of TK
+// keys, the next tile's K and V requested while the current one is used.  Loads put consecutive lanes on
+// consecutive 16-byte pieces, so every load instruction reads 1 KB of whole 128-byte lines: lane l holds dims
+// 8 (l % LPK) .. +8 of key slot l / LPK (LPK = lanes per key row, 8 or 16).  A score is the sum over the LPK lanes
+// of a key slot (DPP, no LDS); its softmax weight is then already in the lanes that hold the same key's V piece,
+// so P*V needs no exchange either.  Each lane keeps its own running (max, sum, 8 output dims); the key slots
+// merge once at the end (lane exchanges), the four waves through LDS.  A single chunk writes the output;
+// otherwise the chunk writes (o, max, sum) partials for attention_combine, as the kernel above.  On MI355X this
+// reads C4's 1.07 GB of K/V per layer at 5.0 TB/s (the tile-per-wave kernel: 3.2 TB/s); with few keys in all
+// (C2) the tile-per-wave kernel's shorter chain wins, so the host picks by the total key count.
+template <int LPK>
+__device__ __forceinline__ float group_sum(float v) {
+    constexpr int kQuadSwap1 = 0xB1, kQuadSwap2 = 0x4E, kHalfMirror = 0x141, kRowMirror = 0x140;
+    auto dpp = [](float x, auto ctrl) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, false));
+    };
+    v += dpp(v, std::integral_constant<int, kQuadSwap1>{});
+    v += dpp(v, std::integral_constant<int, kQuadSwap2>{});
+    v += dpp(v, std::integral_constant<int, kHalfMirror>{});
+    if constexpr (LPK == 16) v += dpp(v, std::integral_constant<int, kRowMirror>{});
+    return v;
+}
+
+template <int HD, int G, int TK>
+__global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_stream(
+    const dlk_attention_params p) {
+    constexpr int W = 4;
+    constexpr int LPK = HD * 2 / 16;        // lanes per key row
+    constexpr int KPI = kWave / LPK;        // keys per load instruction
+    constexpr int NI = TK / KPI;            // load instructions per tile (K, and again V)
+    constexpr int ROW = HD * 2;             // bytes per key row
+    __shared__ float m_s[W][G], l_s[W][G];
+    __shared__ float o_s[W][G][HD];
+
+    const int t = threadIdx.x, lane = t % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int split = blockIdx.x;
+    const int bk = blockIdx.y; // b * KV + kv head
+    const int b = bk / p.KV, kvh = bk % p.KV;
+    const int64_t first = p.position ? *p.position : p.first_host;
+    const int64_t S = first + 1;
+    const int active = static_cast<int>((S + p.chunk - 1) / p.chunk);
+    if (split >= active) {
+        // no keys here: the combine pass gives this slot zero weight
+        if (t < G) {
+            const int64_t slot = (static_cast<int64_t>(b) * p.H + kvh * G + t) * p.splits + split;
+            p.partial_ml[slot * 2] = -INFINITY;
+            p.partial_ml[slot * 2 + 1] = 0.0f;
+        }
+        return;
+    }
+    const int per_wave = p.chunk / W;
+    const int64_t k_end = min(S, static_cast<int64_t>(split) * p.chunk + p.chunk);
+    const int64_t w_begin = static_cast<int64_t>(split) * p.chunk + static_cast<int64_t>(wave) * per_wave;
+    const int keys = static_cast<int>(max<int64_t>(0, min<int64_t>(k_end, w_begin + per_wave) - w_begin));
+    const int tiles = (keys + TK - 1) / TK;
+    const int slot_key = lane / LPK, dc = lane % LPK;
+
+    // q: dims 8 dc .. +8 of the G heads, scaled by scale * log2(e) so that the softmax runs in base 2 (one
+    // v_exp_f32 per weight; the maxima are turned back to natural units for the merges)
+    float q[G][8];
+    {
+        const float qs = p.scale * 1.4426950408889634f;
+        const float* qrow = p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G) * HD + 8 * dc;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float4 a = *reinterpret_cast<const float4*>(qrow + g * HD);
+            const float4 c = *reinterpret_cast<const float4*>(qrow + g * HD + 4);
+            q[g][0] = a.x * qs; q[g][1] = a.y * qs; q[g][2] = a.z * qs; q[g][3] = a.w * qs;
+            q[g][4] = c.x * qs; q[g][5] = c.y * qs; q[g][6] = c.z * qs; q[g][7] = c.w * qs;
+        }
+    }
+    // buffer ranges over this wave's keys: rows past them read as zero (their scores are masked)
+    const size_t head = (static_cast<size_t>(b) * p.KV + kvh) * p.capacity + w_begin;
+    const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.k) + head * HD), 0, keys * ROW, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.v) + head * HD), 0, keys * ROW, kBufferFlags);
+    const int lane_offset = slot_key * ROW + 16 * dc;
+
+    struct Tile {
+        u32x4 k[NI], v[NI];
+    };
+    auto load = [&](int tile, Tile& dst) {
+        const int base = tile * TK * ROW + lane_offset;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) dst.k[i] = __builtin_amdgcn_raw_buffer_load_b128(kres, base + i * KPI * ROW, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) dst.v[i] = __builtin_amdgcn_raw_buffer_load_b128(vres, base + i * KPI * ROW, 0, 0);
+    };
+
+    float m[G], l[G], o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
+    }
+    auto use = [&](int tile, const Tile& cur) {
+        // scores of the lane's NI key slots (identical across the LPK lanes of a slot)
+        float sc[NI][G];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const u32x4 kw = cur.k[i];
+            const float kf[8] = {bf16_lo(kw.x), bf16_hi(kw.x), bf16_lo(kw.y), bf16_hi(kw.y),
+                                 bf16_lo(kw.z), bf16_hi(kw.z), bf16_lo(kw.w), bf16_hi(kw.w)};
+            const bool valid = tile * TK + i * KPI + slot_key < keys;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float part = q[g][0] * kf[0];
+#pragma unroll
+                for (int j = 1; j < 8; ++j) part += q[g][j] * kf[j];
+                const float total = group_sum<LPK>(part);
+                sc[i][g] = valid ? total : -INFINITY;
+            }
+        }
+        // online softmax of the lane's keys, then P*V on the lane's own V pieces
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float tile_max = sc[0][g];
+#pragma unroll
+            for (int i = 1; i < NI; ++i) tile_max = fmaxf(tile_max, sc[i][g]);
+            const float m_new = fmaxf(m[g], tile_max);
+            if (m_new == -INFINITY) continue; // no valid key seen yet in this lane's slots
+            const float alpha = m[g] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[g] - m_new);
+            l[g] *= alpha;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[g][j] *= alpha;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const float pr = sc[i][g] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[i][g] - m_new);
+                l[g] += pr;
+                const u32x4 vw = cur.v[i];
+                o[g][0] += pr * bf16_lo(vw.x); o[g][1] += pr * bf16_hi(vw.x);
+                o[g][2] += pr * bf16_lo(vw.y); o[g][3] += pr * bf16_hi(vw.y);
+                o[g][4] += pr * bf16_lo(vw.z); o[g][5] += pr * bf16_hi(vw.z);
+                o[g][6] += pr * bf16_lo(vw.w); o[g][7] += pr * bf16_hi(vw.w);
+            }
+            m[g] = m_new;
+        }
+    };
+    if (tiles > 0) {
+        Tile a, c;
+        load(0, a);
+        // two tiles per iteration so that the buffers are named statically; the next tile is in flight while one
+        // is used, and no load sits in a branch inside the loop (the last tile is peeled)
+        int tile = 0;
+        for (;;) {
+            if (tile + 1 >= tiles) { use(tile, a); break; }
+            load(tile + 1, c);
+            use(tile, a);
+            ++tile;
+            if (tile + 1 >= tiles) { use(tile, c); break; }
+            load(tile + 1, a);
+            use(tile, c);
+            ++tile;
+        }
+    }
+    // merge the key slots: lanes l and l ^ (LPK, 2 LPK, ...) hold the same dims (symmetric: both lanes get
+    // identical values)
+#pragma unroll
+    for (int off = LPK; off < kWave; off <<= 1) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mo = __shfl_xor(m[g], off, kWave);
+            const float lo = __shfl_xor(l[g], off, kWave);
+            const float mm = fmaxf(m[g], mo);
+            const float a = m[g] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[g] - mm);
+            const float c = mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mm);
+            l[g] = l[g] * a + lo * c;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float oo = __shfl_xor(o[g][j], off, kWave);
+                o[g][j] = o[g][j] * a + oo * c;
+            }
+            m[g] = mm;
+        }
+    }
+    // merge the four waves (the same LDS merge as the tile-per-wave kernel, maxima in natural units)
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            m_s[wave][g] = m[g] * 0.6931471805599453f;
+            l_s[wave][g] = l[g];
+        }
+    }
+    if (lane < LPK) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o_s[wave][g][8 * dc + j] = o[g][j];
+    }
+    lds_barrier();
+    for (int idx = t; idx < G * HD; idx += W * kWave) {
+        const int g = idx / HD, d = idx % HD, h = kvh * G + g;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < W; ++w) M = fmaxf(M, m_s[w][g]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            if (m_s[w][g] == -INFINITY) continue;
+            const float wt = expf(m_s[w][g] - M);
+            L += wt * l_s[w][g];
+            O += wt * o_s[w][g][d];
+        }
+        if (p.splits == 1) {
+            p.out[static_cast<int64_t>(b) * p.ldo + static_cast<int64_t>(h) * HD + d] = O * (1.0f / L);
+        } else {
+            const int64_t slot = (static_cast<int64_t>(b) * p.H + h) * p.splits + split;
+            p.partial_o[slot * HD + d] = O;
+            if (d == 0) {
+                p.partial_ml[slot * 2] = M;
+                p.partial_ml[slot * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+/// Whether the streaming decode kernel serves these heads (bf16 K/V, HD 64 or 128, G = 1, 2 or 4).
+bool stream_heads(int heads, int kv_heads, int hd, int kv_bf16) {
+    if (!kv_bf16 || kv_heads <= 0 || heads % kv_heads != 0 || (hd != 64 && hd != 128)) return false;
+    const int G = heads / kv_heads;
+    return G == 1 || G == 2 || G == 4;
+}
+
+template <int HD, int TK = (HD == 64 ? 32 : 16)>
+int launch_stream(const dlk_attention_params& p, hipStream_t stream) {
+    const dim3 grid(p.splits, p.B * p.KV), block(4 * kWave);
+    switch (p.H / p.KV) {
+    case 1: hipLaunchKernelGGL((attention_stream<HD, 1, TK>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((attention_stream<HD, 2, TK>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((attention_stream<HD, 4, TK>), grid, block, 0, stream, p); break;
+    default: return static_cast<int>(hipErrorInvalidValue);
+    }
+    int status = static_cast<int>(hipGetLastError());
+    if (status != 0 || p.splits == 1 || p.partials_only) return status;
+    const int64_t combine_rows = static_cast<int64_t>(p.B) * p.H;
+    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kThreads), 0, stream, p);
+    return static_cast<int>(hipGetLastError());
+}
+
 /// Widest work-group (waves) each decode variant runs without register spills: a wave may hold 512 / (W / 4)
 /// registers, and the variants need ~90-210 (HD 64) or ~155-335 (HD 128).
 constexpr int decode_waves_max(int hd, int g) {
@@ -552,12 +797,19 @@ extern "C" int dlk_attention_decode_chunk(int heads, int kv_heads, int head_dim,
     return dlk::decode_chunk_max(heads, kv_heads, head_dim, kv_bf16);
 }
 
+extern "C" int dlk_attention_stream_decode(int heads, int kv_heads, int head_dim, int kv_bf16) {
+    return dlk::stream_heads(heads, kv_heads, head_dim, kv_bf16) ? 1 : 0;
+}
+
 extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stream_handle) {
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
     const dlk_attention_params& p = *params;
     if (p.B <= 0 || p.L <= 0 || p.KV <= 0 || p.H % p.KV != 0 || p.splits <= 0 || p.chunk <= 0 ||
         (p.splits > 1 && (!p.partial_o || !p.partial_ml)) || (p.splits > 1 && p.chunk % 64 != 0))
         return static_cast<int>(hipErrorInvalidValue);
+    if (p.L == 1 && dlk::stream_heads(p.H, p.KV, p.hd, p.kv_bf16) && p.chunk % 128 == 0 &&
+        (static_cast<int64_t>(p.B) * p.KV * p.splits * p.chunk >= DLK_STREAM_DECODE_KEYS || !dlk::decode_path(p)))
+        return p.hd == 64 ? dlk::launch_stream<64>(p, stream) : dlk::launch_stream<128>(p, stream);
     if (dlk::decode_path(p)) return p.hd == 64 ? dlk::launch_decode<64>(p, stream) : dlk::launch_decode<128>(p, stream);
     if (dlk_attention_prefill_eligible(&p)) return dlk_attention_prefill(&p, stream_handle);
     if (p.kv_bf16) {

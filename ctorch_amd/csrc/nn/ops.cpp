@@ -2,6 +2,7 @@
 // numeric layer, src/ops/numeric.cpp:178-226,252-254).  Low-precision inputs compute and return f32.
 #include "nn/ops_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <limits>
@@ -81,6 +82,17 @@ void linear_into(const float* x, Index rows, Index k, const Tensor& weight, cons
 void attention_split(Index batch, Index heads, Index kv_heads, Index head_dim, bool kv_bf16, Index length,
                      Index source, int& splits, int& chunk) {
     constexpr Index tile = 64;
+    if (length == 1 && dlk_attention_stream_decode(static_cast<int>(heads), static_cast<int>(kv_heads),
+                                                   static_cast<int>(head_dim), kv_bf16 ? 1 : 0) &&
+        batch * kv_heads * source >= DLK_STREAM_DECODE_KEYS) {
+        // many keys: the streaming kernel, four waves per work-group each streaming its run of keys; runs of
+        // 64..256 keys sized for ~4096 waves in all (measured best at C3 and C4)
+        const Index total = batch * kv_heads * source;
+        const Index per_wave = std::clamp<Index>(((total + 4095) / 4096 + 63) / 64 * 64, 64, 256);
+        chunk = static_cast<int>(4 * per_wave);
+        splits = static_cast<int>((source + chunk - 1) / chunk);
+        return;
+    }
     if (length == 1) {
         // one new position: one 64-key tile per wave, 4..16 waves per work-group merging in LDS; split only
         // beyond the widest work-group (the split partials take a second, combine launch)

@@ -271,6 +271,38 @@ def test_decode_over_split_keys_merges_partials():
     assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
 
 
+@pytest.mark.parametrize("dimensions,heads,kv_heads", [(512, 8, 2), (512, 8, 4), (512, 8, 8), (1024, 8, 2)])
+def test_streaming_decode_attention_over_many_keys(dimensions, heads, kv_heads):
+    # B * KV * prefix >= 32768 keys in all: one-position steps take the streaming decode kernel (4 waves per
+    # work-group, each streaming its run of keys, key splits merged by the combine launch)
+    B, P = 8, 2100
+    say(f"case: streaming decode attention, d={dimensions} heads={heads}/{kv_heads}, B={B}, {P}-token prefix")
+    cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=dimensions, heads=heads, kv_heads=kv_heads, hidden=512,
+                             context=P + 24, dtype="bf16")
+    assert B * kv_heads * P >= 32768
+    ref, gpu = build_pair(cfg, root=(61, 0), scale=0.04)
+    hd = cfg.head_dim
+    rc, gc = ref.make_cache(B), gpu.cache()
+    for layer in range(cfg.layers):
+        k = oracle.randn(oracle.fold_in((83, 0), 2 * layer), B * kv_heads * P * hd).reshape(B, kv_heads, P, hd)
+        v = oracle.randn(oracle.fold_in((83, 0), 2 * layer + 1), B * kv_heads * P * hd).reshape(B, kv_heads, P, hd)
+        kb, vb = oracle.bf16_encode(k), oracle.bf16_encode(v)
+        gc.append(layer, ct.Tensor.from_numpy(kb, ct.BF16, GPU), ct.Tensor.from_numpy(vb, ct.BF16, GPU))
+        rc.fill(layer, P, oracle.bf16_decode(kb), oracle.bf16_decode(vb))
+    ids = oracle.random_ids((84, 0), B, cfg.vocab).reshape(B, 1)
+    for step in range(3):
+        want = ref.logits(ids, rc)[:, -1]
+        got = gpu.logits(ids, gc)
+        assert np.max(np.abs(got - want)) <= 2e-2, step
+        ids = want.argmax(-1).reshape(B, 1)
+    # graph replay (splits sized for the capacity, chunks past the length idle) equals eager
+    gc.truncate(P)
+    t1, l1 = gpu.generate(ids, 8, 0.0, (0, 0), use_graph=True, cache=gc)
+    gc.truncate(P)
+    t2, l2 = gpu.generate(ids, 8, 0.0, (0, 0), use_graph=False, cache=gc)
+    assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
+
+
 def test_prefill_on_tiled_matrix_cores_with_lora_and_causal_attention():
     say("case: bf16 prefill B=2 x 2048, d=1024 (tiled projections + matrix-core causal attention), LoRA q/v")
     cfg = oracle.ModelConfig(vocab=512, layers=1, dimensions=1024, heads=16, kv_heads=4, hidden=2816, context=2056,
