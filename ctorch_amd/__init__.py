@@ -20,7 +20,7 @@ LIB_PATH = os.path.join(_HERE, "libctorch_amd.so")
 
 F32, F64, I64, BOOL, F16, BF16 = 0, 1, 2, 3, 4, 5
 CPU, GPU = 0, 1
-_NP = {F32: np.float32, F64: np.float64, I64: np.int64, BOOL: np.bool_, BF16: np.uint16}
+_NP = {F32: np.float32, F64: np.float64, I64: np.int64, BOOL: np.bool_, F16: np.uint16, BF16: np.uint16}
 
 
 class DLError(RuntimeError):
@@ -116,6 +116,8 @@ SIGNATURES = {
     "dl_state_name": (C.c_char_p, [_p, C.c_size_t]),
     "dl_state_tensor": (_st, [_p, C.c_size_t, _pp]),
     "dl_state_create": (_st, [C.POINTER(C.c_char_p), C.POINTER(_p), C.c_size_t, _pp]),
+    "dl_state_save": (_st, [C.c_char_p, _p]),
+    "dl_state_load": (_st, [C.c_char_p, _pp]),
     # decoder_c_api.h
     "dl_tensordot": (_st, [_p, _p, Shape, Shape, _pp]),
     "dl_rotary_embedding": (_st, [_p, _p, _p, _pp]),
@@ -215,9 +217,10 @@ class Tensor:
         if dtype is None:
             dtype = {np.dtype(np.float32): F32, np.dtype(np.float64): F64, np.dtype(np.int64): I64,
                      np.dtype(np.bool_): BOOL, np.dtype(np.uint16): BF16}[array.dtype]
+        shape = array.shape  # np.ascontiguousarray turns a rank-0 array into rank 1
         array = np.ascontiguousarray(array, _NP[dtype])
         out = C.c_void_p()
-        check(lib().dl_from_host(array.ctypes.data_as(C.c_void_p), _shape(array.shape), options(dtype, dev),
+        check(lib().dl_from_host(array.ctypes.data_as(C.c_void_p), _shape(shape), options(dtype, dev),
                                  C.byref(out)))
         return Tensor(out)
 
@@ -295,6 +298,37 @@ class Module:
             check(lib().dl_module_load_state(self.handle, st))
         finally:
             lib().dl_state_release(st)
+
+
+def _state_handle(values: dict[str, np.ndarray | Tensor], dtypes: dict[str, int] | None = None) -> C.c_void_p:
+    names, tensors = [], []
+    for name, value in values.items():
+        if not isinstance(value, Tensor):
+            value = Tensor.from_numpy(value, (dtypes or {}).get(name), device("cpu"))
+        names.append(name)
+        tensors.append(value)
+    c_names = (C.c_char_p * len(names))(*[n.encode() for n in names])
+    c_tensors = (C.c_void_p * len(tensors))(*[t.handle.value for t in tensors])
+    return _new(lib().dl_state_create, c_names, c_tensors, len(names))
+
+
+def save_state(path: str, values: dict[str, np.ndarray | Tensor], dtypes: dict[str, int] | None = None) -> None:
+    """dl_state_save: the named tensors as a version-1 Ctorch tensor archive (`.ct`)."""
+    st = _state_handle(values, dtypes)
+    try:
+        check(lib().dl_state_save(str(path).encode(), st))
+    finally:
+        lib().dl_state_release(st)
+
+
+def load_state(path: str) -> dict[str, Tensor]:
+    """dl_state_load: the archive's named tensors, on the CPU, in file order."""
+    st = _new(lib().dl_state_load, str(path).encode())
+    try:
+        return {lib().dl_state_name(st, i).decode(): Tensor(_new(lib().dl_state_tensor, st, i))
+                for i in range(lib().dl_state_size(st))}
+    finally:
+        lib().dl_state_release(st)
 
 
 def transformer_decoder(layers, dimensions, heads, kv_heads, hidden, context, dtype=F32, dev=None,

@@ -1,5 +1,6 @@
-// Module and state entries of <dl/c_api.h> (reference src/api/module.cpp:31,44,167,201-216, src/api/state.cpp:66,79).
+// Module and state entries of <dl/c_api.h> (reference src/api/module.cpp:31,44,167,201-216, src/api/state.cpp:66-80).
 #include "api/common.h"
+#include "dl/io.h"
 
 #include <stdexcept>
 
@@ -88,6 +89,20 @@ dl_status dl_state_tensor(const dl_state* state, size_t index, dl_tensor** outpu
         const auto& s = require(state, "state").value;
         if (index >= s.size()) throw std::out_of_range("state index out of range");
         return s[index].second;
+    });
+}
+
+dl_status dl_state_save(const char* path, const dl_state* state) {
+    return invoke([&] {
+        if (!path) throw std::invalid_argument("path must be non-NULL");
+        dl::io::save(path, require(state, "state").value);
+    });
+}
+
+dl_status dl_state_load(const char* path, dl_state** output) {
+    return make_handle(output, [&] {
+        if (!path) throw std::invalid_argument("path must be non-NULL");
+        return dl::io::load(path);
     });
 }
 

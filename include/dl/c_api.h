@@ -122,6 +122,9 @@ DL_API const char* dl_state_name(const dl_state* state, size_t index);
 DL_API dl_status dl_state_tensor(const dl_state* state, size_t index, dl_tensor** output);
 DL_API dl_status dl_state_create(const char* const* names, const dl_tensor* const* tensors, size_t count,
     dl_state** output);
+/* c_api.h:647-648: the named state as a version-1 tensor archive (dl/io.h); load gives CPU tensors */
+DL_API dl_status dl_state_save(const char* path, const dl_state* state);
+DL_API dl_status dl_state_load(const char* path, dl_state** output);
 
 #ifdef __cplusplus
 }
