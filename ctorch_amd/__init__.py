@@ -94,6 +94,8 @@ SIGNATURES = {
     "dl_rms_norm": (_st, [_p, Shape, _p, C.POINTER(_f64), _pp]),
     "dl_synchronize": (_st, [Device]),
     "dl_gpu_memory_get_stats": (_st, [_i32, C.POINTER(MemoryStats)]),
+    "dl_gpu_memory_set_release_threshold": (_st, [_i32, C.c_uint64]),
+    "dl_gpu_memory_reset_peak_stats": (_st, [_i32]),
     "dl_gpu_memory_release_unused": (_st, [_i32]),
     "dl_random_fold_in": (RandomKey, [RandomKey, C.c_uint64]),
     "dl_random_split": (None, [RandomKey, C.c_size_t, C.POINTER(RandomKey)]),
@@ -138,6 +140,8 @@ SIGNATURES = {
     "dl_transformer_decoder_create_with_base": (_st, [_i64, _i64, _i64, _i64, _i64, _i64, _f64, TensorOptions, _pp]),
     "dl_transformer_decoder_attach_lora": (_st, [_p, _i64, _f64, _i32, _i32]),
     "dl_decoder_cache_append": (_st, [_p, _i64, _p, _p]),
+    "dl_decoder_cache_state": (_st, [_p, _pp]),
+    "dl_decoder_cache_load_state": (_st, [_p, _p, _p]),
     # generate_c_api.h
     "dl_decoder_lm_create": (_st, [_p, _p, _p, _pp]),
     "dl_decoder_lm_release": (None, [_p]),
@@ -195,6 +199,28 @@ def _shape(dims) -> Shape:
 
 def device(kind: str = "gpu", index: int = 0) -> Device:
     return Device(GPU if kind == "gpu" else CPU, index)
+
+
+def memory_stats(index: int = 0) -> MemoryStats:
+    """dl_gpu_memory_get_stats: the device pool's used / reserved bytes and their peaks."""
+    out = MemoryStats()
+    check(lib().dl_gpu_memory_get_stats(index, C.byref(out)))
+    return out
+
+
+def set_release_threshold(bytes_: int, index: int = 0) -> None:
+    """dl_gpu_memory_set_release_threshold: free bytes above this go back to the device at synchronisation."""
+    check(lib().dl_gpu_memory_set_release_threshold(index, bytes_))
+
+
+def reset_peak_stats(index: int = 0) -> None:
+    """dl_gpu_memory_reset_peak_stats: restarts both peaks (from zero, as HIP does)."""
+    check(lib().dl_gpu_memory_reset_peak_stats(index))
+
+
+def release_unused(index: int = 0) -> None:
+    """dl_gpu_memory_release_unused: returns the pool's free blocks to the device."""
+    check(lib().dl_gpu_memory_release_unused(index))
 
 
 def options(dtype: int = F32, dev: Device | None = None) -> TensorOptions:
@@ -369,6 +395,23 @@ class DecoderCache:
 
     def clear(self) -> None:
         check(lib().dl_decoder_cache_clear(self.handle))
+
+    def state(self) -> dict[str, Tensor]:
+        """dl_decoder_cache_state: past_key_i / past_value_i, f32 [B, KV, length, hd] (the ONNX wire format)."""
+        st = _new(lib().dl_decoder_cache_state, self.handle)
+        try:
+            return {lib().dl_state_name(st, i).decode(): Tensor(_new(lib().dl_state_tensor, st, i))
+                    for i in range(lib().dl_state_size(st))}
+        finally:
+            lib().dl_state_release(st)
+
+    def load_state(self, decoder: "Module", values: dict[str, np.ndarray | Tensor]) -> None:
+        """dl_decoder_cache_load_state: replaces the cache's contents with past_* (or present_*) tensors."""
+        st = _state_handle(values)
+        try:
+            check(lib().dl_decoder_cache_load_state(decoder.handle, self.handle, st))
+        finally:
+            lib().dl_state_release(st)
 
     def append(self, layer: int, key: Tensor, value: Tensor) -> None:
         check(lib().dl_decoder_cache_append(self.handle, layer, key.handle, value.handle))

@@ -1,6 +1,7 @@
 // Entries of <dl/decoder_c_api.h> (reference src/api/decoder.cpp:4-70).
 #include "api/common.h"
 #include "core/tensor_impl.h"
+#include "nn/decode_step.h"
 
 #include <numeric>
 #include <stdexcept>
@@ -177,6 +178,70 @@ dl_status dl_decoder_cache_append(dl_decoder_cache* cache, int64_t layer, const 
         auto& layers = require(cache, "cache").value;
         if (layer < 0 || layer >= static_cast<int64_t>(layers.size())) throw std::out_of_range("cache layer out of range");
         layers[static_cast<std::size_t>(layer)].append(require(key, "key").value, require(value, "value").value);
+    });
+}
+
+dl_status dl_decoder_cache_state(const dl_decoder_cache* cache, dl_state** output) {
+    return make_handle(output, [&] {
+        const auto& layers = require(cache, "cache").value;
+        dl::StateDict state;
+        for (std::size_t i = 0; i < layers.size(); ++i) {
+            if (!layers[i].reserved())
+                throw std::logic_error("cache layer " + std::to_string(i) + " holds no keys yet (its batch is unknown)");
+            state.emplace_back("past_key_" + std::to_string(i), layers[i].key().astype(dl::DType::f32).contiguous());
+            state.emplace_back("past_value_" + std::to_string(i), layers[i].value().astype(dl::DType::f32).contiguous());
+        }
+        return state;
+    });
+}
+
+dl_status dl_decoder_cache_load_state(const dl_module* decoder, dl_decoder_cache* cache, const dl_state* state) {
+    return invoke([&] {
+        const auto& dec = as<dl::nn::TransformerDecoder>(decoder, "TransformerDecoder");
+        auto& layers = require(cache, "cache").value;
+        const auto& entries = require(state, "state").value;
+        if (layers.size() != static_cast<std::size_t>(dec.layer_count()))
+            throw std::invalid_argument("cache and decoder have different layer counts");
+        auto find = [&](const std::string& kind, std::size_t layer) -> const dl::Tensor& {
+            const dl::Tensor* found = nullptr;
+            for (const char* prefix : {"past_", "present_"}) {
+                const std::string name = prefix + kind + "_" + std::to_string(layer);
+                for (const auto& [n, t] : entries) {
+                    if (n != name) continue;
+                    if (found) throw std::invalid_argument("cache state names layer " + std::to_string(layer) + " " +
+                                                           kind + " twice");
+                    found = &t;
+                }
+            }
+            if (!found) throw std::invalid_argument("cache state has no past_" + kind + "_" + std::to_string(layer));
+            return *found;
+        };
+        // validate every layer before touching the cache
+        std::vector<std::pair<const dl::Tensor*, const dl::Tensor*>> kv;
+        dl::Index batch = -1, length = -1;
+        for (std::size_t i = 0; i < layers.size(); ++i) {
+            const auto& attention = dec.layer(static_cast<dl::Index>(i)).attention();
+            const dl::Tensor& k = find("key", i);
+            const dl::Tensor& v = find("value", i);
+            for (const dl::Tensor* t : {&k, &v})
+                if (t->ndim() != 4 || t->size(1) != attention.kv_heads() || t->size(3) != attention.head_dim())
+                    throw std::invalid_argument("cache state layer " + std::to_string(i) +
+                                                " must be [batch, kv_heads, length, head_dim]");
+            if (k.shape() != v.shape()) throw std::invalid_argument("cache state key and value shapes differ");
+            if (batch < 0) { batch = k.size(0); length = k.size(2); }
+            if (k.size(0) != batch || k.size(2) != length)
+                throw std::invalid_argument("cache state layers must share batch and length");
+            if (length > layers[i].capacity()) throw std::invalid_argument("cache state exceeds the cache capacity");
+            kv.emplace_back(&k, &v);
+        }
+        for (std::size_t i = 0; i < layers.size(); ++i) {
+            const auto& layer = dec.layer(static_cast<dl::Index>(i));
+            const auto& attention = layer.attention();
+            const dl::Device device = attention.query().weight().device();
+            layers[i] = dl::nn::KVCache(layers[i].capacity());
+            layers[i].reserve(batch, attention.kv_heads(), attention.head_dim(), dl::detail::cache_dtype(layer), device);
+            layers[i].append(kv[i].first->to(device), kv[i].second->to(device));
+        }
     });
 }
 

@@ -2,6 +2,7 @@
 // 465,581-586, src/api/statistics.cpp:16-22).
 #include "api/common.h"
 #include "core/tensor_impl.h"
+#include "dl/gpu.h"
 
 #include <cstring>
 #include <string>
@@ -144,20 +145,23 @@ dl_status dl_synchronize(dl_device device) { return invoke([&] { dl::synchronize
 
 dl_status dl_gpu_memory_get_stats(int32_t device, dl_gpu_memory_stats* output) {
     return invoke([&] {
-        dl::detail::gpu_context(device);
-        dl::detail::hip_check(dlh_pool_stats(device, &output->used_bytes, &output->reserved_bytes,
-                                             &output->peak_used_bytes, &output->peak_reserved_bytes,
-                                             &output->release_threshold),
-                              "pool statistics");
+        if (!output) throw std::invalid_argument("memory statistics output is null");
+        const auto stats = dl::gpu::memory_stats(device);
+        *output = {stats.used_bytes, stats.reserved_bytes, stats.peak_used_bytes, stats.peak_reserved_bytes,
+                   stats.release_threshold};
     });
 }
 
+dl_status dl_gpu_memory_set_release_threshold(int32_t device, uint64_t bytes) {
+    return invoke([&] { dl::gpu::set_memory_release_threshold(bytes, device); });
+}
+
+dl_status dl_gpu_memory_reset_peak_stats(int32_t device) {
+    return invoke([&] { dl::gpu::reset_peak_memory_stats(device); });
+}
+
 dl_status dl_gpu_memory_release_unused(int32_t device) {
-    return invoke([&] {
-        auto& context = dl::detail::gpu_context(device);
-        dl::detail::hip_check(dlh_stream_synchronize(context.stream), "synchronize");
-        dl::detail::hip_check(dlh_pool_trim(device), "pool trim");
-    });
+    return invoke([&] { dl::gpu::release_unused_memory(device); });
 }
 
 dl_random_key dl_random_fold_in(dl_random_key key, uint64_t label) { return convert(dl::fold_in(convert(key), label)); }

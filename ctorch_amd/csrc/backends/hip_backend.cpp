@@ -86,6 +86,23 @@ int dlh_pool_trim(int device) {
     return code(hipMemPoolTrimTo(pool, 0));
 }
 
+int dlh_pool_set_threshold(int device, uint64_t bytes) {
+    hipMemPool_t pool;
+    hipError_t e = hipDeviceGetDefaultMemPool(&pool, device);
+    if (e != hipSuccess) return code(e);
+    return code(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &bytes));
+}
+
+int dlh_pool_reset_peaks(int device) {
+    hipMemPool_t pool;
+    hipError_t e = hipDeviceGetDefaultMemPool(&pool, device);
+    if (e != hipSuccess) return code(e);
+    uint64_t zero = 0; // the high-water attributes accept only zero
+    e = hipMemPoolSetAttribute(pool, hipMemPoolAttrUsedMemHigh, &zero);
+    if (e == hipSuccess) e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReservedMemHigh, &zero);
+    return code(e);
+}
+
 int dlh_memcpy_async(void* destination, const void* source, size_t bytes, int kind, dlh_stream stream) {
     hipMemcpyKind k = kind == DLH_HOST_TO_DEVICE   ? hipMemcpyHostToDevice
                       : kind == DLH_DEVICE_TO_HOST ? hipMemcpyDeviceToHost

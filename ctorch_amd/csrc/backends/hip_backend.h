@@ -50,6 +50,8 @@ int dlh_free_async(void* pointer, dlh_stream stream);
 int dlh_pool_stats(int device, uint64_t* used, uint64_t* reserved, uint64_t* peak_used, uint64_t* peak_reserved,
                    uint64_t* threshold);
 int dlh_pool_trim(int device);
+int dlh_pool_set_threshold(int device, uint64_t bytes);
+int dlh_pool_reset_peaks(int device);
 
 int dlh_memcpy_async(void* destination, const void* source, size_t bytes, int kind, dlh_stream stream);
 

@@ -1,5 +1,7 @@
 #include "core/device.h"
 
+#include "dl/gpu.h"
+
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -112,3 +114,30 @@ void synchronize(Device device) {
     detail::hip_check(dlh_stream_synchronize(context.stream), "synchronize");
 }
 } // namespace dl
+
+namespace dl::gpu {
+MemoryStats memory_stats(int device) {
+    detail::gpu_context(device);
+    MemoryStats out{};
+    detail::hip_check(dlh_pool_stats(device, &out.used_bytes, &out.reserved_bytes, &out.peak_used_bytes,
+                                     &out.peak_reserved_bytes, &out.release_threshold),
+                      "pool statistics");
+    return out;
+}
+
+void set_memory_release_threshold(std::uint64_t bytes, int device) {
+    detail::gpu_context(device);
+    detail::hip_check(dlh_pool_set_threshold(device, bytes), "pool release threshold");
+}
+
+void reset_peak_memory_stats(int device) {
+    detail::gpu_context(device);
+    detail::hip_check(dlh_pool_reset_peaks(device), "pool peak reset");
+}
+
+void release_unused_memory(int device) {
+    auto& context = detail::gpu_context(device);
+    detail::hip_check(dlh_stream_synchronize(context.stream), "synchronize");
+    detail::hip_check(dlh_pool_trim(device), "pool trim");
+}
+} // namespace dl::gpu

@@ -89,6 +89,8 @@ DL_API dl_status dl_rms_norm(const dl_tensor* input, dl_shape normalized_shape,
 /* c_api.h:489-499: device synchronisation and allocator statistics (renamed from dl_cuda_memory_*) */
 DL_API dl_status dl_synchronize(dl_device device);
 DL_API dl_status dl_gpu_memory_get_stats(int32_t device, dl_gpu_memory_stats* output);
+DL_API dl_status dl_gpu_memory_set_release_threshold(int32_t device, uint64_t bytes);
+DL_API dl_status dl_gpu_memory_reset_peak_stats(int32_t device);
 DL_API dl_status dl_gpu_memory_release_unused(int32_t device);
 
 /* c_api.h:512-521: explicit-key randomness */

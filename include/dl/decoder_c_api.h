@@ -55,6 +55,14 @@ DL_API dl_status dl_transformer_decoder_create_with_base(int64_t layers, int64_t
  * layer{i}.attention.{query,value}_adapter.{down,up}.weight. */
 DL_API dl_status dl_transformer_decoder_attach_lora(dl_module* decoder, int64_t rank, double alpha,
     int32_t query, int32_t value);
+/* The ONNX decoder's cache wire format (reference extensions/onnx/src/decoder.cpp:64-69, docs/onnx.md:68-113):
+ * per layer i, past_key_i / past_value_i as f32 [batch, kv_heads, length, head_dim].  cache_state writes the
+ * cache under those names (ready to feed an ONNX Runtime session as its next past_* inputs).  cache_load_state
+ * replaces the cache's contents with such a state; each layer may be named past_* or present_* (an ONNX
+ * session's outputs), all layers must share batch and length, and the values are stored in the decoder's cache
+ * dtype.  Nothing changes when the state does not fit (chunk-atomic). */
+DL_API dl_status dl_decoder_cache_state(const dl_decoder_cache* cache, dl_state** output);
+DL_API dl_status dl_decoder_cache_load_state(const dl_module* decoder, dl_decoder_cache* cache, const dl_state* state);
 /* Extension: writes the K and V of one layer's cache directly (keys already rotated), the reference's
  * KVCache::append route (include/dl/decoder.h:52) for seeding a prefix.  key/value are [B, KV, n, D]. */
 DL_API dl_status dl_decoder_cache_append(dl_decoder_cache* cache, int64_t layer, const dl_tensor* key,

@@ -359,3 +359,76 @@ def test_c2_1b_shape_bf16_decode_parity():
         assert row[got_tokens[0, step]] >= row.max() - 4e-2
     sampled, logits = gpu.generate(prompt, 3, 1.0, (99, 1))
     assert np.array_equal(oracle.sample(logits, 1.0, oracle.fold_in((99, 1), 2)), sampled[:, -1])
+
+
+# ------------------------------------------------------------------------------------------ cache wire format
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_cache_state_export_matches_the_oracle_and_import_continues_the_decode(dtype):
+    say(f"case: {dtype} cache exported as past_key_i / past_value_i after a 9-token prompt, imported, 2 more steps")
+    cfg = oracle.ModelConfig(vocab=256, layers=2, dimensions=256, heads=8, kv_heads=2, hidden=512, context=32,
+                             dtype=dtype)
+    ref, gpu = build_pair(cfg, root=(61, 0), scale=0.05)
+    prompt = oracle.random_ids((62, 0), 2 * 9, cfg.vocab).reshape(2, 9)
+    rc, gc = ref.make_cache(2), gpu.cache()
+    ref.logits(prompt, rc)
+    gpu.logits(prompt, gc)
+    state = {name: t.numpy() for name, t in gc.state().items()}
+    assert sorted(state) == sorted(f"past_{kind}_{i}" for i in range(cfg.layers) for kind in ("key", "value"))
+    for i in range(cfg.layers):
+        for kind, want in (("key", rc.keys[i]), ("value", rc.values[i])):
+            got = state[f"past_{kind}_{i}"]
+            assert got.shape == (2, cfg.kv_heads, 9, cfg.head_dim)
+            if dtype == "f32":
+                assert rel_err(got, want[:, :, :9]) <= 1e-4, (kind, i)
+            else:
+                assert np.max(np.abs(got - want[:, :, :9])) <= 2e-2, (kind, i)
+    copy = gpu.cache()
+    copy.load_state(gpu.decoder, state)
+    assert copy.length == 9
+    assert all(np.array_equal(t.numpy(), state[n]) for n, t in copy.state().items())
+    ids = oracle.random_ids((63, 0), 2, cfg.vocab).reshape(2, 1)
+    for step in range(2):
+        a = gpu.logits(ids, gc)
+        b = gpu.logits(ids, copy)
+        assert np.array_equal(a, b), step  # the same cache contents give the same decode, bit for bit
+        ids = a.argmax(-1).reshape(2, 1)
+
+
+# ------------------------------------------------------------------------------------------ device migration
+def test_decoder_built_on_the_host_moves_to_the_gpu_and_its_memory_returns_to_the_pool():
+    say("case: f32 decoder loaded on the host, Module::to(gpu), decode vs oracle, pool statistics and trim")
+    cfg = oracle.ModelConfig(vocab=64, layers=2, dimensions=128, heads=4, kv_heads=2, hidden=256, context=16,
+                             dtype="f32")
+    weights = oracle.synthesize_weights(cfg, (71, 0), 0.1)
+    ref = oracle.OracleLM(cfg, weights)
+    dec = ct.transformer_decoder(cfg.layers, cfg.dimensions, cfg.heads, cfg.kv_heads, cfg.hidden, cfg.context,
+                                 ct.F32, ct.device("cpu"), cfg.rope_base)
+    state = {name[len("decoder."):]: value for name, value in weights.items() if name.startswith("decoder.")}
+    for name, tensor in dec.state().items():
+        state.setdefault(name, tensor)
+    dec.load_state(state)
+    weight_bytes = sum(v.nbytes for v in state.values() if isinstance(v, np.ndarray))
+    ct.release_unused()
+    before = ct.memory_stats()
+    dec.to(GPU)
+    moved = ct.memory_stats()
+    assert moved.used_bytes - before.used_bytes >= weight_bytes
+    x = np.random.default_rng(12).standard_normal((2, 5, cfg.dimensions)).astype(np.float32)
+    want = ref.decode(x, ref.make_cache(2))
+    got = ct.decode(dec, G(x), ct.DecoderCache(dec)).numpy()
+    assert rel_err(got, want) <= 1e-5
+    del dec
+    ct.release_unused()
+    after = ct.memory_stats()
+    assert after.used_bytes <= moved.used_bytes - weight_bytes
+    assert after.reserved_bytes <= moved.reserved_bytes and after.peak_used_bytes >= moved.used_bytes
+    ct.reset_peak_stats()
+    reset = ct.memory_stats()
+    assert reset.peak_used_bytes < moved.used_bytes  # HIP restarts the high-water marks at zero
+    block = G(np.zeros(1 << 18, np.float32))
+    assert ct.memory_stats().peak_used_bytes >= reset.used_bytes + block.numpy().nbytes
+    keep = after.release_threshold
+    ct.set_release_threshold(1 << 20)
+    assert ct.memory_stats().release_threshold == 1 << 20
+    ct.set_release_threshold(keep)
+    assert ct.memory_stats().release_threshold == keep
