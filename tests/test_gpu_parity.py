@@ -432,3 +432,25 @@ def test_decoder_built_on_the_host_moves_to_the_gpu_and_its_memory_returns_to_th
     assert ct.memory_stats().release_threshold == 1 << 20
     ct.set_release_threshold(keep)
     assert ct.memory_stats().release_threshold == keep
+
+
+# ------------------------------------------------------------------------------------------ forward without a cache
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_forward_without_a_cache_over_a_sequence_the_reference_would_block(dtype):
+    # TransformerDecoder::forward (reference src/nn/decoder.cpp:116-120) runs causal attention over the whole
+    # input; at B=1, H=8, S=2048 the reference splits the queries into blocks of (8 Mi / (B*H*S)) = 512 rows
+    # (src/ops/attention.cpp:59-63), which leaves the result unchanged.
+    say(f"case: {dtype} TransformerDecoder::forward on [1, 2048, 256], no cache, vs the oracle's prefill")
+    cfg = oracle.ModelConfig(vocab=64, layers=2, dimensions=256, heads=8, kv_heads=2, hidden=512, context=2048,
+                             dtype=dtype)
+    ref, gpu = build_pair(cfg, root=(81, 0), scale=0.05)
+    x = np.random.default_rng(13).standard_normal((1, 2048, cfg.dimensions)).astype(np.float32)
+    want = ref.decode(x, ref.make_cache(1))
+    got = gpu.decoder.forward(G(x)).numpy()
+    assert got.shape == want.shape
+    if dtype == "f32":
+        assert rel_err(got, want) <= 1e-4
+    else:
+        assert np.max(np.abs(got - want)) <= 2e-2
+    again = gpu.decoder.forward(G(x)).numpy()
+    assert np.array_equal(again, got)  # no state is kept between calls
