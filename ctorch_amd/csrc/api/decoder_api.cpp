@@ -188,8 +188,12 @@ dl_status dl_decoder_cache_state(const dl_decoder_cache* cache, dl_state** outpu
         for (std::size_t i = 0; i < layers.size(); ++i) {
             if (!layers[i].reserved())
                 throw std::logic_error("cache layer " + std::to_string(i) + " holds no keys yet (its batch is unknown)");
-            state.emplace_back("past_key_" + std::to_string(i), layers[i].key().astype(dl::DType::f32).contiguous());
-            state.emplace_back("past_value_" + std::to_string(i), layers[i].value().astype(dl::DType::f32).contiguous());
+            // a snapshot: an f32 cache's contiguous prefix would otherwise come back as a view of live storage
+            auto snapshot = [](const dl::Tensor& t) {
+                return t.dtype() == dl::DType::f32 ? t.clone() : t.astype(dl::DType::f32);
+            };
+            state.emplace_back("past_key_" + std::to_string(i), snapshot(layers[i].key()));
+            state.emplace_back("past_value_" + std::to_string(i), snapshot(layers[i].value()));
         }
         return state;
     });

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdio>
 #include <cstring>
 
 namespace {
@@ -31,8 +32,8 @@ int dlh_device_properties_get(int device, dlh_device_properties* out) {
     const hipError_t e = hipGetDeviceProperties(&p, device);
     if (e != hipSuccess) return code(e);
     std::memset(out, 0, sizeof(*out));
-    std::strncpy(out->name, p.name, sizeof(out->name) - 1);
-    std::strncpy(out->arch, p.gcnArchName, sizeof(out->arch) - 1);
+    std::snprintf(out->name, sizeof(out->name), "%s", p.name);
+    std::snprintf(out->arch, sizeof(out->arch), "%s", p.gcnArchName);
     out->compute_units = p.multiProcessorCount;
     out->wavefront_size = p.warpSize;
     out->clock_khz = p.clockRate;

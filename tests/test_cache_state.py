@@ -82,3 +82,20 @@ def test_cache_state_errors_leave_the_cache_unchanged():
         assert np.array_equal(out[name].numpy(), want), name
     with pytest.raises(ct.DLError, match="no keys yet"):
         ct.DecoderCache(dec).state()
+
+
+def test_cache_state_is_a_snapshot_of_a_full_f32_cache():
+    # at full capacity (and with one sequence and one KV head) the valid prefix is contiguous storage
+    rng = np.random.default_rng(8)
+    dec = ct.transformer_decoder(1, 32, 2, 1, 48, 6, ct.F32, ct.device("cpu"))
+    cache = ct.DecoderCache(dec)
+    first = past_state(rng, 1, 1, 1, 6, 16)
+    cache.load_state(dec, first)
+    exported = cache.state()
+    cache.truncate(0)  # rewrite the same storage in place
+    other = past_state(rng, 1, 1, 1, 6, 16)
+    cache.append(0, ct.Tensor.from_numpy(other["past_key_0"], ct.F32, ct.device("cpu")),
+                 ct.Tensor.from_numpy(other["past_value_0"], ct.F32, ct.device("cpu")))
+    assert np.array_equal(cache.state()["past_key_0"].numpy(), other["past_key_0"])
+    for name, want in first.items():
+        assert np.array_equal(exported[name].numpy(), want), name
