@@ -32,8 +32,8 @@ int dlh_device_properties_get(int device, dlh_device_properties* out) {
     const hipError_t e = hipGetDeviceProperties(&p, device);
     if (e != hipSuccess) return code(e);
     std::memset(out, 0, sizeof(*out));
-    std::snprintf(out->name, sizeof(out->name), "%s", p.name);
-    std::snprintf(out->arch, sizeof(out->arch), "%s", p.gcnArchName);
+    std::snprintf(out->name, sizeof(out->name), "%.*s", static_cast<int>(sizeof(out->name) - 1), p.name);
+    std::snprintf(out->arch, sizeof(out->arch), "%.*s", static_cast<int>(sizeof(out->arch) - 1), p.gcnArchName);
     out->compute_units = p.multiProcessorCount;
     out->wavefront_size = p.warpSize;
     out->clock_khz = p.clockRate;
