@@ -136,17 +136,26 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
         p.y[static_cast<int64_t>(m) * p.ldy + n] = gemv::silu(v[0]) * v[1];
         p.y[static_cast<int64_t>(m) * p.ldy + n + 1] = gemv::silu(v[2]) * v[3];
     } else if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL) {
+        // every operand is loaded before the first store: y may alias them as far as the compiler knows, so a
+        // load issued after a store waits for it, and the four outputs would take four memory round trips
+        float add[4] = {0.f, 0.f, 0.f, 0.f};
+        const bool bias = EPI == DLK_EPI_STORE && p.bias;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = t.n0 + 4 * q + j;
+            if constexpr (EPI == DLK_EPI_STORE) {
+                if (bias)
+                    add[j] = p.bias_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.bias)[n])
+                                         : static_cast<const float*>(p.bias)[n];
+            } else {
+                add[j] = p.residual[static_cast<int64_t>(m) * p.ldres + n];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int n = t.n0 + 4 * q + j;
             float out = v[j];
-            if constexpr (EPI == DLK_EPI_STORE) {
-                if (p.bias)
-                    out += p.bias_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.bias)[n])
-                                       : static_cast<const float*>(p.bias)[n];
-            } else {
-                out += p.residual[static_cast<int64_t>(m) * p.ldres + n];
-            }
+            if (EPI == DLK_EPI_RESIDUAL || bias) out += add[j];
             p.y[static_cast<int64_t>(m) * p.ldy + n] = out;
         }
     } else if constexpr (EPI == DLK_EPI_QKV) {
@@ -156,6 +165,17 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
         const int hd = p.head_dim;
         const float* hidden = t.seg == 0 ? p.lora_hidden[0] : t.seg == 2 ? p.lora_hidden[2] : nullptr;
         const void* lora_up = t.seg == 0 ? p.lora_up[0] : p.lora_up[2];
+        // the rotation of both pairs is loaded before any store (see the residual epilogue above)
+        float rc[2] = {1.f, 1.f}, rs[2] = {0.f, 0.f};
+        if (t.seg < 2) {
+#pragma unroll
+            for (int pair = 0; pair < 2; ++pair) {
+                const int d = (t.n0 + 4 * q + 2 * pair) % hd;
+                const int64_t table = pos * (hd / 2) + d / 2;
+                rc[pair] = p.cosine[table];
+                rs[pair] = p.sine[table];
+            }
+        }
 #pragma unroll
         for (int pair = 0; pair < 2; ++pair) {
             const int n = t.n0 + 4 * q + 2 * pair; // even: the pair (n, n + 1) shares one rotation
@@ -177,8 +197,7 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
             const int d = n % hd, head = n / hd;
             if (t.seg < 2) {
                 // even: x_e c - x_o s ; odd: x_e s + x_o c (interleaved pairs, src/ops/contraction.cpp:44-49)
-                const int64_t table = pos * (hd / 2) + d / 2;
-                const float c = p.cosine[table], s = p.sine[table];
+                const float c = rc[pair], s = rs[pair];
                 const float re = even * c - odd * s, ro = even * s + odd * c;
                 even = re;
                 odd = ro;
