@@ -454,3 +454,23 @@ def test_forward_without_a_cache_over_a_sequence_the_reference_would_block(dtype
         assert np.max(np.abs(got - want)) <= 2e-2
     again = gpu.decoder.forward(G(x)).numpy()
     assert np.array_equal(again, got)  # no state is kept between calls
+
+
+# ------------------------------------------------------------------------------------------ tensor archives
+def test_gpu_decoder_state_saved_to_an_archive_loads_into_a_fresh_gpu_decoder(tmp_path):
+    say("case: bf16 GPU decoder state -> .ct archive -> fresh GPU decoder, decode bit for bit")
+    cfg = oracle.ModelConfig(vocab=256, layers=2, dimensions=256, heads=8, kv_heads=2, hidden=512, context=32,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(91, 0), scale=0.05)
+    path = tmp_path / "decoder.ct"
+    ct.save_state(str(path), gpu.decoder.state())  # device tensors are copied to the host by the save
+    loaded = ct.load_state(str(path))
+    assert all(t.info.device.type == ct.CPU for t in loaded.values())
+    fresh = ct.transformer_decoder(cfg.layers, cfg.dimensions, cfg.heads, cfg.kv_heads, cfg.hidden, cfg.context,
+                                   ct.BF16, GPU, cfg.rope_base)
+    fresh.load_state(loaded)
+    x = np.random.default_rng(14).standard_normal((2, 6, cfg.dimensions)).astype(np.float32)
+    a = ct.decode(gpu.decoder, G(x), ct.DecoderCache(gpu.decoder)).numpy()
+    b = ct.decode(fresh, G(x), ct.DecoderCache(fresh)).numpy()
+    assert np.array_equal(a, b)
+    assert np.max(np.abs(a - ref.decode(x, ref.make_cache(2)))) <= 2e-2
