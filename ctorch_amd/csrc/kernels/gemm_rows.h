@@ -246,7 +246,9 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
     constexpr int ROWS_PER_PASS = kThreads / COLS;
     constexpr int XR = RM / ROWS_PER_PASS; // staging loads per thread per chunk
     static_assert(RM % ROWS_PER_PASS == 0, "staging covers the rows");
-    extern __shared__ uint16_t lds[];      // [2 buffers][hi, lo][RM][STRIDE]
+    // the dynamic LDS follows the static variables below: their sizes are multiples of 16 bytes, and the
+    // alignment is stated, because its 128-bit reads run at half speed or worse when misaligned
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[]; // [2 buffers][hi, lo][RM][STRIDE]
     __shared__ float row_squares[RM];
     __shared__ double pool_score[kWaves][RM];
     __shared__ int64_t pool_index[kWaves][RM];
