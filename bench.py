@@ -64,13 +64,14 @@ def parameter_slots(cfg):
     return names
 
 
-def build_model(ct, cfg, context, root=(1234, 0), dtype=None):
+def build_model(ct, cfg, context, root=(1234, 0), dtype=None, kv_dtype=None):
     """Seeded weights drawn directly in HBM: slot s gets 0.02 * randn(fold_in(root, s)) rounded to bf16 (LoRA up
-    matrices 1e-3 * randn); unmerged LoRA adapters on q and v when cfg has lora_rank."""
+    matrices 1e-3 * randn); unmerged LoRA adapters on q and v when cfg has lora_rank.  The K/V cache is f32 (the
+    reference's dtype) unless kv_dtype asks for bf16."""
     gpu = ct.device("gpu")
     dtype = ct.BF16 if dtype is None else dtype
     decoder = ct.transformer_decoder(cfg["layers"], cfg["dimensions"], cfg["heads"], cfg["kv_heads"], cfg["hidden"],
-                                     context, dtype, gpu, cfg.get("rope_base", 10000.0))
+                                     context, dtype, gpu, cfg.get("rope_base", 10000.0), kv_dtype=kv_dtype)
     if cfg.get("lora_rank"):
         ct.check(ct.lib().dl_transformer_decoder_attach_lora(decoder.handle, cfg["lora_rank"], cfg["lora_alpha"], 1, 1))
     state, embedding, head = {}, None, None
@@ -101,9 +102,10 @@ def weight_bytes(cfg):
     return 2 * (cfg["layers"] * per_layer + V * d)  # LM head once; one embedding row per sequence is negligible
 
 
-def kv_bytes(cfg, batch, length):
+def kv_bytes(cfg, batch, length, element=4):
+    """K and V read per step: f32 (4 bytes) for the reference's cache dtype, 2 for the bf16 opt-in."""
     hd = cfg["dimensions"] // cfg["heads"]
-    return 2 * batch * cfg["layers"] * 2 * cfg["kv_heads"] * hd * length  # bf16 K and V read
+    return element * batch * cfg["layers"] * 2 * cfg["kv_heads"] * hd * length
 
 
 def decode_b1(ct, steps, warmup):
@@ -125,9 +127,10 @@ def decode_b1(ct, steps, warmup):
 
 
 def decode_b32(ct, steps, warmup, prefix=2048):
-    """C3: batch 32, each sequence holding `prefix` cached tokens of seeded random K/V."""
+    """C3: batch 32, each sequence holding `prefix` cached tokens of seeded random K/V in the bf16 cache opt-in
+    (the KV-bandwidth regime BASELINE sizes in bf16)."""
     B = 32
-    decoder, lm = build_model(ct, C2, prefix + 3 + warmup + steps + 8)
+    decoder, lm = build_model(ct, C2, prefix + 3 + warmup + steps + 8, kv_dtype=ct.BF16)
     cache = ct.DecoderCache(decoder)
     hd = C2["dimensions"] // C2["heads"]
     for layer in range(C2["layers"]):
@@ -138,14 +141,14 @@ def decode_b32(ct, steps, warmup, prefix=2048):
     ids = np.random.default_rng(8).integers(0, C2["vocab"], size=(B, 1), dtype=np.int64)
     ms, _ = lm.benchmark(ids, cache, warmup, steps, 0.0, (0, 0), True)
     mean_len = prefix + 3 + warmup + (steps - 1) / 2.0
-    return dict(ms=ms, step_bytes=weight_bytes(C2) + kv_bytes(C2, B, mean_len), batch=B, mean_len=mean_len)
+    return dict(ms=ms, step_bytes=weight_bytes(C2) + kv_bytes(C2, B, mean_len, 2), batch=B, mean_len=mean_len)
 
 
 def decode_c4(ct, steps, warmup, batch=8, prefix=32768):
     """C4: the 8B-class decoder (RoPE base 500000), batch 8, each sequence holding `prefix` cached positions of
-    seeded random K/V (34 GB of bf16 KV at 32768), greedy decode."""
+    seeded random K/V (34 GB in the bf16 cache opt-in at 32768), greedy decode."""
     cfg = C4
-    decoder, lm = build_model(ct, cfg, prefix + 3 + warmup + steps + 8, root=(88, 0))
+    decoder, lm = build_model(ct, cfg, prefix + 3 + warmup + steps + 8, root=(88, 0), kv_dtype=ct.BF16)
     cache = ct.DecoderCache(decoder)
     hd = cfg["dimensions"] // cfg["heads"]
     for layer in range(cfg["layers"]):
@@ -156,7 +159,7 @@ def decode_c4(ct, steps, warmup, batch=8, prefix=32768):
     ids = np.random.default_rng(9).integers(0, cfg["vocab"], size=(batch, 1), dtype=np.int64)
     ms, _ = lm.benchmark(ids, cache, warmup, steps, 0.0, (0, 0), True)
     mean_len = prefix + 3 + warmup + (steps - 1) / 2.0
-    return dict(ms=ms, step_bytes=weight_bytes(cfg) + kv_bytes(cfg, batch, mean_len), batch=batch, mean_len=mean_len)
+    return dict(ms=ms, step_bytes=weight_bytes(cfg) + kv_bytes(cfg, batch, mean_len, 2), batch=batch, mean_len=mean_len)
 
 
 def prefill_flops(cfg, batch, length):

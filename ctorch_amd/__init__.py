@@ -140,6 +140,8 @@ SIGNATURES = {
     "dl_transformer_decoder_create_with_base": (_st, [_i64, _i64, _i64, _i64, _i64, _i64, _f64, TensorOptions, _pp]),
     "dl_transformer_decoder_attach_lora": (_st, [_p, _i64, _f64, _i32, _i32]),
     "dl_decoder_cache_append": (_st, [_p, _i64, _p, _p]),
+    "dl_transformer_decoder_set_cache_dtype": (_st, [_p, C.c_int]),
+    "dl_transformer_decoder_cache_dtype": (_st, [_p, C.POINTER(C.c_int)]),
     "dl_decoder_cache_state": (_st, [_p, _pp]),
     "dl_decoder_cache_load_state": (_st, [_p, _p, _p]),
     # generate_c_api.h
@@ -358,13 +360,24 @@ def load_state(path: str) -> dict[str, Tensor]:
 
 
 def transformer_decoder(layers, dimensions, heads, kv_heads, hidden, context, dtype=F32, dev=None,
-                        rope_base: float = 10000.0) -> Module:
+                        rope_base: float = 10000.0, kv_dtype: int | None = None) -> Module:
+    """TransformerDecoder; kv_dtype (F32 default, or BF16) is the K/V storage dtype of its decode."""
     opts = options(dtype, dev if dev is not None else device("cpu"))
     if rope_base == 10000.0:
-        return Module(_new(lib().dl_transformer_decoder_create, layers, dimensions, heads, kv_heads, hidden, context,
-                           opts))
-    return Module(_new(lib().dl_transformer_decoder_create_with_base, layers, dimensions, heads, kv_heads, hidden,
-                       context, rope_base, opts))
+        module = Module(_new(lib().dl_transformer_decoder_create, layers, dimensions, heads, kv_heads, hidden, context,
+                             opts))
+    else:
+        module = Module(_new(lib().dl_transformer_decoder_create_with_base, layers, dimensions, heads, kv_heads, hidden,
+                             context, rope_base, opts))
+    if kv_dtype is not None:
+        check(lib().dl_transformer_decoder_set_cache_dtype(module.handle, kv_dtype))
+    return module
+
+
+def cache_dtype(decoder: Module) -> int:
+    out = C.c_int()
+    check(lib().dl_transformer_decoder_cache_dtype(decoder.handle, C.byref(out)))
+    return out.value
 
 
 def embedding_from(weight: Tensor) -> Module:

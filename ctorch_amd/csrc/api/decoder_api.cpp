@@ -146,6 +146,18 @@ dl_status dl_transformer_decoder_attach_lora(dl_module* decoder, int64_t rank, d
     });
 }
 
+dl_status dl_transformer_decoder_set_cache_dtype(dl_module* decoder, dl_dtype dtype) {
+    return invoke([&] {
+        as<dl::nn::TransformerDecoder>(decoder, "TransformerDecoder").set_cache_dtype(static_cast<dl::DType>(dtype));
+    });
+}
+
+dl_status dl_transformer_decoder_cache_dtype(const dl_module* decoder, dl_dtype* dtype) {
+    return invoke([&] {
+        *dtype = static_cast<dl_dtype>(as<dl::nn::TransformerDecoder>(decoder, "TransformerDecoder").cache_dtype());
+    });
+}
+
 dl_status dl_decoder_cache_create(const dl_module* decoder, dl_decoder_cache** output) {
     return make_handle(output, [&] { return as<dl::nn::TransformerDecoder>(decoder, "TransformerDecoder").make_cache(); });
 }
@@ -242,9 +254,10 @@ dl_status dl_decoder_cache_load_state(const dl_module* decoder, dl_decoder_cache
             const auto& layer = dec.layer(static_cast<dl::Index>(i));
             const auto& attention = layer.attention();
             const dl::Device device = attention.query().weight().device();
+            const dl::DType dtype = dl::detail::cache_dtype(layer);
             layers[i] = dl::nn::KVCache(layers[i].capacity());
-            layers[i].reserve(batch, attention.kv_heads(), attention.head_dim(), dl::detail::cache_dtype(layer), device);
-            layers[i].append(kv[i].first->to(device), kv[i].second->to(device));
+            layers[i].reserve(batch, attention.kv_heads(), attention.head_dim(), dtype, device);
+            layers[i].append(kv[i].first->to(device).astype(dtype), kv[i].second->to(device).astype(dtype));
         }
     });
 }

@@ -224,7 +224,10 @@ __global__ __launch_bounds__(kThreads) void attention_combine(const dlk_attentio
     float acc = 0.0f, total = 0.0f;
     for (int s = group; s < p.splits; s += GROUPS) {
         const float ms = ml[2 * s], ls = ml[2 * s + 1];
-        const float w = ls > 0.0f && ms != -INFINITY ? expf(ms - maximum) : 0.0f;
+        // a split without keys has weight 0 and an unwritten partial_o row: it must not enter the sum (0 * a
+        // stale NaN or Inf would)
+        if (!(ls > 0.0f && ms != -INFINITY)) continue;
+        const float w = expf(ms - maximum);
         total += w * ls;
         acc += w * p.partial_o[(prow * p.splits + s) * HD + d];
     }
@@ -244,29 +247,67 @@ __global__ __launch_bounds__(kThreads) void attention_combine(const dlk_attentio
 }
 
 // ------------------------------------------------------------------------------------------ decode
-// One new position per sequence (L = 1) over bf16 K/V, G = H/KV query heads per KV head.  A work-group of W
+// One new position per sequence (L = 1) over bf16 or f32 K/V, G = H/KV query heads per KV head.  A work-group of W
 // waves takes one (sequence, KV head, key chunk of 64 W keys); each wave one 64-key tile of the chunk, loaded
 // straight into registers when the kernel starts (no dependency precedes them): the K rows with one lane per
-// key for the scores, the V rows with one lane per pair of head-dim columns for P*V.  The scaled q rows are
-// broadcast from LDS.  Each wave normalises its tile on its own (max, exp, sum); the W waves merge through
-// LDS.  A single chunk writes the output; with several, each writes (o, max, sum) partials (empty ones a
-// zero weight) and attention_combine merges them in fixed order in the next launch.
+// key for the scores, the V rows with one lane per CPL head-dim columns for P*V (two bf16 columns per 32-bit
+// load, four f32 columns per 16-byte load).  The scaled q rows are broadcast from LDS.  Each wave normalises its
+// tile on its own (max, exp, sum); the W waves merge through LDS.  A single chunk writes the output; with
+// several, each writes (o, max, sum) partials (empty ones a zero weight) and attention_combine merges them in
+// fixed order in the next launch.
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int HD, int G, int W>
+/// The head-dim values of one 16-byte piece of a K/V row: 8 bf16 or 4 f32.
+template <typename KT>
+__device__ __forceinline__ void unpack16(const u32x4 w, float (&f)[16 / sizeof(KT)]) {
+    if constexpr (sizeof(KT) == 2) {
+        f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x); f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+        f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z); f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+    } else {
+        f[0] = __uint_as_float(w.x); f[1] = __uint_as_float(w.y); f[2] = __uint_as_float(w.z);
+        f[3] = __uint_as_float(w.w);
+    }
+}
+
+template <typename KT> struct DecodeV;
+template <> struct DecodeV<uint16_t> { // two bf16 columns per lane, one 32-bit load
+    static constexpr int CPL = 2;
+    using Word = uint32_t;
+    __device__ static __forceinline__ Word load(__amdgpu_buffer_rsrc_t r, int offset, int soffset) {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, offset, soffset, 0);
+    }
+    __device__ static __forceinline__ void unpack(Word w, float (&f)[CPL]) { f[0] = bf16_lo(w); f[1] = bf16_hi(w); }
+};
+template <> struct DecodeV<float> { // four f32 columns per lane, one 16-byte load
+    static constexpr int CPL = 4;
+    using Word = u32x4;
+    __device__ static __forceinline__ Word load(__amdgpu_buffer_rsrc_t r, int offset, int soffset) {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, offset, soffset, 0);
+    }
+    __device__ static __forceinline__ void unpack(Word w, float (&f)[CPL]) {
+        f[0] = __uint_as_float(w.x); f[1] = __uint_as_float(w.y); f[2] = __uint_as_float(w.z);
+        f[3] = __uint_as_float(w.w);
+    }
+};
+
+template <typename KT, int HD, int G, int W>
 __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_decode(
     const dlk_attention_params p) {
     constexpr int kThreads = W * kWave;
-    constexpr int KCH = HD * 2 / 16;  // 16-byte chunks of a K row
-    constexpr int DL = HD / 2;        // lanes per V row (two bf16 columns per lane)
+    constexpr int ES = sizeof(KT);
+    constexpr int DPC = 16 / ES;      // head-dim values per 16-byte piece
+    constexpr int KCH = HD / DPC;     // 16-byte pieces of a K row
+    constexpr int CPL = DecodeV<KT>::CPL;
+    constexpr int DL = HD / CPL;      // lanes per V row
     constexpr int KP = kWave / DL;    // keys per V load instruction
     constexpr int VL = kWave / KP;    // V loads per lane for a 64-key tile
     constexpr int QN = (G * HD + kThreads - 1) / kThreads;
     static_assert(DL <= kWave && kWave % DL == 0, "a V row must fit one wave");
+    using VWord = typename DecodeV<KT>::Word;
     __shared__ float q_s[G][HD];
     __shared__ float p_s[W][kWave][G];
     __shared__ float m_s[W][G], l_s[W][G];
@@ -294,8 +335,8 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
     const int64_t k_end = min(S, k_begin + p.chunk);
     const int64_t key0 = k_begin + static_cast<int64_t>(kWave) * wave;
     const size_t head = (static_cast<size_t>(b) * p.KV + kvh) * p.capacity;
-    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + head * HD;
-    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + head * HD;
+    const KT* kbase = static_cast<const KT*>(p.k) + head * HD;
+    const KT* vbase = static_cast<const KT*>(p.v) + head * HD;
 
     // q first, then K and V (vector loads complete in issue order: the q wait never covers K/V).  Keys past
     // the chunk end are clamped to its last key; their scores are masked.
@@ -308,20 +349,20 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
     // buffer loads over this wave's tile: offsets are immediates or scalars, and rows past the chunk end read
     // as zero (their scores are masked below)
     u32x4 kr[KCH];
-    uint32_t vr[VL];
+    VWord vr[VL];
     {
-        const int bytes = static_cast<int>(max<int64_t>(0, k_end - key0)) * HD * 2;
+        const int bytes = static_cast<int>(max<int64_t>(0, k_end - key0)) * HD * ES;
         const __amdgpu_buffer_rsrc_t kres =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase + key0 * HD), 0, bytes, kBufferFlags);
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<KT*>(kbase + key0 * HD), 0, bytes, kBufferFlags);
         const __amdgpu_buffer_rsrc_t vres =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase + key0 * HD), 0, bytes, kBufferFlags);
-        const int krow = lane * HD * 2;
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<KT*>(vbase + key0 * HD), 0, bytes, kBufferFlags);
+        const int krow = lane * HD * ES;
 #pragma unroll
         for (int c = 0; c < KCH; ++c) kr[c] = __builtin_amdgcn_raw_buffer_load_b128(kres, krow + c * 16, 0, 0);
         __builtin_amdgcn_sched_barrier(0); // K is issued (and so completes) before V: the scores wait for K only
-        const int vlane = (lane / DL) * HD * 2 + (lane % DL) * 4;
+        const int vlane = (lane / DL) * HD * ES + (lane % DL) * CPL * ES;
 #pragma unroll
-        for (int j = 0; j < VL; ++j) vr[j] = __builtin_amdgcn_raw_buffer_load_b32(vres, vlane, j * KP * HD * 2, 0);
+        for (int j = 0; j < VL; ++j) vr[j] = DecodeV<KT>::load(vres, vlane, j * KP * HD * ES);
     }
 #pragma unroll
     for (int i = 0; i < QN; ++i) {
@@ -330,39 +371,42 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
     }
     lds_barrier();
 
-    // scores: lane = key.  The q values of chunk c + 1 are read from LDS (broadcast) while chunk c is used: a
-    // batch of 2G reads in flight instead of one read at a time.
+    // scores: lane = key.  The q values of piece c + 1 are read from LDS (broadcast) while piece c is used: a
+    // batch of G DPC reads in flight instead of one read at a time.
+    constexpr int Q4 = DPC / 4; // float4 reads of q per piece and head
     const bool valid = key0 + lane < k_end;
     float sc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) sc[g] = 0.0f;
-    float4 qc[G][2], qn[G][2];
-    auto read_q = [&](int c, float4 (&dst)[G][2]) {
+    float4 qc[G][Q4], qn[G][Q4];
+    auto read_q = [&](int c, float4 (&dst)[G][Q4]) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            dst[g][0] = *reinterpret_cast<const float4*>(&q_s[g][c * 8]);
-            dst[g][1] = *reinterpret_cast<const float4*>(&q_s[g][c * 8 + 4]);
-        }
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < Q4; ++j) dst[g][j] = *reinterpret_cast<const float4*>(&q_s[g][c * DPC + 4 * j]);
     };
     read_q(0, qc);
 #pragma unroll
     for (int c = 0; c < KCH; ++c) {
         if (c + 1 < KCH) read_q(c + 1, qn);
         __builtin_amdgcn_sched_barrier(0);
-        const float kf[8] = {bf16_lo(kr[c].x), bf16_hi(kr[c].x), bf16_lo(kr[c].y), bf16_hi(kr[c].y),
-                             bf16_lo(kr[c].z), bf16_hi(kr[c].z), bf16_lo(kr[c].w), bf16_hi(kr[c].w)};
+        float kf[DPC];
+        unpack16<KT>(kr[c], kf);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float4 qa = qc[g][0], qb = qc[g][1];
-            sc[g] += qa.x * kf[0] + qa.y * kf[1] + qa.z * kf[2] + qa.w * kf[3] + qb.x * kf[4] + qb.y * kf[5] +
-                     qb.z * kf[6] + qb.w * kf[7];
+            float part = 0.0f;
+#pragma unroll
+            for (int j = 0; j < Q4; ++j) {
+                const float4 qa = qc[g][j];
+                part += qa.x * kf[4 * j] + qa.y * kf[4 * j + 1] + qa.z * kf[4 * j + 2] + qa.w * kf[4 * j + 3];
+            }
+            sc[g] += part;
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            qc[g][0] = qn[g][0];
-            qc[g][1] = qn[g][1];
-        }
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < Q4; ++j) qc[g][j] = qn[g][j];
     }
     // the wave's softmax over its tile
     float m_w[G], l_w[G];
@@ -377,13 +421,15 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 
-    // P*V: lane = (column pair lane % DL, key class lane / DL); the P values of the next PB keys are read from
+    // P*V: lane = (column group lane % DL, key class lane / DL); the P values of the next PB keys are read from
     // LDS while the current ones are used
     constexpr int PB = HD * G > 256 ? 4 : 8; // smaller batches keep the widest variants under 256 registers
     static_assert(VL % PB == 0, "P batches");
-    float o[G][2];
+    float o[G][CPL];
 #pragma unroll
-    for (int g = 0; g < G; ++g) o[g][0] = o[g][1] = 0.0f;
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) o[g][c] = 0.0f;
     float pc[PB][G], pn[PB][G];
     auto read_p = [&](int j0, float (&dst)[PB][G]) {
 #pragma unroll
@@ -411,12 +457,12 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < PB; ++i) {
-            const float lo = bf16_lo(vr[j0 + i]), hi = bf16_hi(vr[j0 + i]);
+            float vf[CPL];
+            DecodeV<KT>::unpack(vr[j0 + i], vf);
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                o[g][0] += pc[i][g] * lo;
-                o[g][1] += pc[i][g] * hi;
-            }
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) o[g][c] += pc[i][g] * vf[c];
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -427,10 +473,9 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
 #pragma unroll
     for (int off = DL; off < kWave; off <<= 1)
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            o[g][0] += __shfl_xor(o[g][0], off, kWave);
-            o[g][1] += __shfl_xor(o[g][1], off, kWave);
-        }
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) o[g][c] += __shfl_xor(o[g][c], off, kWave);
 
     // merge the W waves
     if (lane == 0) {
@@ -442,10 +487,9 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
     }
     if (lane < DL) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            o_s[wave][g][2 * lane] = o[g][0];
-            o_s[wave][g][2 * lane + 1] = o[g][1];
-        }
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) o_s[wave][g][CPL * lane + c] = o[g][c];
     }
     lds_barrier();
     for (int idx = t; idx < G * HD; idx += kThreads) {
@@ -475,13 +519,14 @@ __global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
 }
 
 // ------------------------------------------------------------------------------------------ streaming decode
-// One new position per sequence (L = 1) over bf16 K/V, HD 64 or 128, G = H/KV <= 4.  A work-group of four
+// One new position per sequence (L = 1) over bf16 or f32 K/V, HD 64 or 128, G = H/KV <= 4.  A work-group of four
 // waves takes one (sequence, KV head, key chunk); each wave streams its own run of chunk / 4 keys in tiles of TK
 // keys, the next tile's K and V requested while the current one is used.  Loads put consecutive lanes on
-// consecutive 16-byte pieces, so every load instruction reads 1 KB of whole 128-byte lines: lane l holds dims
-// 8 (l % LPK) .. +8 of key slot l / LPK (LPK = lanes per key row, 8 or 16).  A score is the sum over the LPK lanes
-// of a key slot (DPP, no LDS); its softmax weight is then already in the lanes that hold the same key's V piece,
-// so P*V needs no exchange either.  Each lane keeps its own running (max, sum, 8 output dims); the key slots
+// consecutive 16-byte pieces, so every load instruction reads 1 KB of whole 128-byte lines: lane l holds the DPL
+// dims DPL (l % LPK) .. +DPL of key slot l / LPK (DPL = 8 bf16 or 4 f32 values; LPK = lanes per key row, 8 to 32).
+// A score is the sum over the LPK lanes of a key slot (DPP within 16-lane rows, a lane swap across two rows, no
+// LDS); its softmax weight is then already in the lanes that hold the same key's V piece, so P*V needs no
+// exchange either.  Each lane keeps its own running (max, sum, DPL output dims); the key slots
 // merge once at the end (lane exchanges), the four waves through LDS.  A single chunk writes the output;
 // otherwise the chunk writes (o, max, sum) partials for attention_combine, as the kernel above.  On MI355X this
 // reads C4's 1.07 GB of K/V per layer at 5.0 TB/s (the tile-per-wave kernel: 3.2 TB/s); with few keys in all
@@ -495,18 +540,26 @@ __device__ __forceinline__ float group_sum(float v) {
     v += dpp(v, std::integral_constant<int, kQuadSwap1>{});
     v += dpp(v, std::integral_constant<int, kQuadSwap2>{});
     v += dpp(v, std::integral_constant<int, kHalfMirror>{});
-    if constexpr (LPK == 16) v += dpp(v, std::integral_constant<int, kRowMirror>{});
+    if constexpr (LPK >= 16) v += dpp(v, std::integral_constant<int, kRowMirror>{});
+    if constexpr (LPK == 32) {
+        // rows 2i and 2i + 1 exchange their values in registers: both receive the pair's sum
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
     return v;
 }
 
-template <int HD, int G, int TK>
+template <typename KT, int HD, int G, int TK>
 __global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_stream(
     const dlk_attention_params p) {
     constexpr int W = 4;
-    constexpr int LPK = HD * 2 / 16;        // lanes per key row
+    constexpr int ES = sizeof(KT);
+    constexpr int DPL = 16 / ES;            // head-dim values per lane (one 16-byte piece)
+    constexpr int LPK = HD * ES / 16;       // lanes per key row
     constexpr int KPI = kWave / LPK;        // keys per load instruction
     constexpr int NI = TK / KPI;            // load instructions per tile (K, and again V)
-    constexpr int ROW = HD * 2;             // bytes per key row
+    constexpr int ROW = HD * ES;            // bytes per key row
+    static_assert(NI >= 1 && TK % KPI == 0, "whole load instructions per tile");
     __shared__ float m_s[W][G], l_s[W][G];
     __shared__ float o_s[W][G][HD];
 
@@ -534,26 +587,26 @@ __global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
     const int tiles = (keys + TK - 1) / TK;
     const int slot_key = lane / LPK, dc = lane % LPK;
 
-    // q: dims 8 dc .. +8 of the G heads, scaled by scale * log2(e) so that the softmax runs in base 2 (one
+    // q: dims DPL dc .. +DPL of the G heads, scaled by scale * log2(e) so that the softmax runs in base 2 (one
     // v_exp_f32 per weight; the maxima are turned back to natural units for the merges)
-    float q[G][8];
+    float q[G][DPL];
     {
         const float qs = p.scale * 1.4426950408889634f;
-        const float* qrow = p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G) * HD + 8 * dc;
+        const float* qrow = p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G) * HD + DPL * dc;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float4 a = *reinterpret_cast<const float4*>(qrow + g * HD);
-            const float4 c = *reinterpret_cast<const float4*>(qrow + g * HD + 4);
-            q[g][0] = a.x * qs; q[g][1] = a.y * qs; q[g][2] = a.z * qs; q[g][3] = a.w * qs;
-            q[g][4] = c.x * qs; q[g][5] = c.y * qs; q[g][6] = c.z * qs; q[g][7] = c.w * qs;
-        }
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < DPL; j += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(qrow + g * HD + j);
+                q[g][j] = a.x * qs; q[g][j + 1] = a.y * qs; q[g][j + 2] = a.z * qs; q[g][j + 3] = a.w * qs;
+            }
     }
     // buffer ranges over this wave's keys: rows past them read as zero (their scores are masked)
     const size_t head = (static_cast<size_t>(b) * p.KV + kvh) * p.capacity + w_begin;
     const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.k) + head * HD), 0, keys * ROW, kBufferFlags);
+        const_cast<KT*>(static_cast<const KT*>(p.k) + head * HD), 0, keys * ROW, kBufferFlags);
     const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.v) + head * HD), 0, keys * ROW, kBufferFlags);
+        const_cast<KT*>(static_cast<const KT*>(p.v) + head * HD), 0, keys * ROW, kBufferFlags);
     const int lane_offset = slot_key * ROW + 16 * dc;
 
     struct Tile {
@@ -567,28 +620,27 @@ __global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
         for (int i = 0; i < NI; ++i) dst.v[i] = __builtin_amdgcn_raw_buffer_load_b128(vres, base + i * KPI * ROW, 0, 0);
     };
 
-    float m[G], l[G], o[G][8];
+    float m[G], l[G], o[G][DPL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
         l[g] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[g][j] = 0.0f;
+        for (int j = 0; j < DPL; ++j) o[g][j] = 0.0f;
     }
     auto use = [&](int tile, const Tile& cur) {
         // scores of the lane's NI key slots (identical across the LPK lanes of a slot)
         float sc[NI][G];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const u32x4 kw = cur.k[i];
-            const float kf[8] = {bf16_lo(kw.x), bf16_hi(kw.x), bf16_lo(kw.y), bf16_hi(kw.y),
-                                 bf16_lo(kw.z), bf16_hi(kw.z), bf16_lo(kw.w), bf16_hi(kw.w)};
+            float kf[DPL];
+            unpack16<KT>(cur.k[i], kf);
             const bool valid = tile * TK + i * KPI + slot_key < keys;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float part = q[g][0] * kf[0];
 #pragma unroll
-                for (int j = 1; j < 8; ++j) part += q[g][j] * kf[j];
+                for (int j = 1; j < DPL; ++j) part += q[g][j] * kf[j];
                 const float total = group_sum<LPK>(part);
                 sc[i][g] = valid ? total : -INFINITY;
             }
@@ -604,16 +656,15 @@ __global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
             const float alpha = m[g] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[g] - m_new);
             l[g] *= alpha;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o[g][j] *= alpha;
+            for (int j = 0; j < DPL; ++j) o[g][j] *= alpha;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const float pr = sc[i][g] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[i][g] - m_new);
                 l[g] += pr;
-                const u32x4 vw = cur.v[i];
-                o[g][0] += pr * bf16_lo(vw.x); o[g][1] += pr * bf16_hi(vw.x);
-                o[g][2] += pr * bf16_lo(vw.y); o[g][3] += pr * bf16_hi(vw.y);
-                o[g][4] += pr * bf16_lo(vw.z); o[g][5] += pr * bf16_hi(vw.z);
-                o[g][6] += pr * bf16_lo(vw.w); o[g][7] += pr * bf16_hi(vw.w);
+                float vf[DPL];
+                unpack16<KT>(cur.v[i], vf);
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) o[g][j] += pr * vf[j];
             }
             m[g] = m_new;
         }
@@ -648,7 +699,7 @@ __global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
             const float c = mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mm);
             l[g] = l[g] * a + lo * c;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < DPL; ++j) {
                 const float oo = __shfl_xor(o[g][j], off, kWave);
                 o[g][j] = o[g][j] * a + oo * c;
             }
@@ -667,7 +718,7 @@ __global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) o_s[wave][g][8 * dc + j] = o[g][j];
+            for (int j = 0; j < DPL; ++j) o_s[wave][g][DPL * dc + j] = o[g][j];
     }
     lds_barrier();
     for (int idx = t; idx < G * HD; idx += W * kWave) {
@@ -696,20 +747,22 @@ __global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
     }
 }
 
-/// Whether the streaming decode kernel serves these heads (bf16 K/V, HD 64 or 128, G = 1, 2 or 4).
+/// Whether the streaming decode kernel serves these heads (bf16 or f32 K/V, HD 64 or 128, G = 1, 2 or 4).
 bool stream_heads(int heads, int kv_heads, int hd, int kv_bf16) {
-    if (!kv_bf16 || kv_heads <= 0 || heads % kv_heads != 0 || (hd != 64 && hd != 128)) return false;
+    (void)kv_bf16;
+    if (kv_heads <= 0 || heads % kv_heads != 0 || (hd != 64 && hd != 128)) return false;
     const int G = heads / kv_heads;
     return G == 1 || G == 2 || G == 4;
 }
 
-template <int HD, int TK = (HD == 64 ? 32 : 16)>
+// Keys per tile: 32 bf16 / 16 f32 keys at HD 64, half that at HD 128 (the same 4 KB of K and of V per tile)
+template <typename KT, int HD, int TK = (HD == 64 ? 32 : 16) * 2 / static_cast<int>(sizeof(KT))>
 int launch_stream(const dlk_attention_params& p, hipStream_t stream) {
     const dim3 grid(p.splits, p.B * p.KV), block(4 * kWave);
     switch (p.H / p.KV) {
-    case 1: hipLaunchKernelGGL((attention_stream<HD, 1, TK>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((attention_stream<HD, 2, TK>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((attention_stream<HD, 4, TK>), grid, block, 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((attention_stream<KT, HD, 1, TK>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((attention_stream<KT, HD, 2, TK>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((attention_stream<KT, HD, 4, TK>), grid, block, 0, stream, p); break;
     default: return static_cast<int>(hipErrorInvalidValue);
     }
     int status = static_cast<int>(hipGetLastError());
@@ -720,18 +773,21 @@ int launch_stream(const dlk_attention_params& p, hipStream_t stream) {
 }
 
 /// Widest work-group (waves) each decode variant runs without register spills: a wave may hold 512 / (W / 4)
-/// registers, and the variants need ~90-210 (HD 64) or ~155-335 (HD 128).
-constexpr int decode_waves_max(int hd, int g) {
+/// registers, and the bf16 variants need ~90-210 (HD 64) or ~155-335 (HD 128).  f32 K/V hold twice the K and V
+/// bytes per lane (64 + 64 registers at HD 64): at most eight waves, four at G = 8; f32 at HD 128 takes the
+/// streaming kernel.
+constexpr int decode_waves_max(int hd, int g, bool f32) {
+    if (f32) return hd == 64 ? (g <= 4 ? 8 : 4) : 0;
     return hd == 64 ? (g <= 2 ? 16 : 8) : (g <= 2 ? 8 : 4);
 }
 
-template <int HD, int W>
+template <typename KT, int HD, int W>
 int launch_decode_w(const dlk_attention_params& p, hipStream_t stream) {
     const dim3 grid(p.splits, p.B * p.KV), block(W * kWave);
     auto go = [&](auto g) {
         constexpr int G = decltype(g)::value;
-        if constexpr (W <= decode_waves_max(HD, G) && !(HD == 128 && G > 4)) {
-            hipLaunchKernelGGL((attention_decode<HD, G, W>), grid, block, 0, stream, p);
+        if constexpr (W <= decode_waves_max(HD, G, sizeof(KT) == 4) && !(HD == 128 && G > 4)) {
+            hipLaunchKernelGGL((attention_decode<KT, HD, G, W>), grid, block, 0, stream, p);
             return static_cast<int>(hipGetLastError());
         }
         return static_cast<int>(hipErrorInvalidValue);
@@ -745,13 +801,18 @@ int launch_decode_w(const dlk_attention_params& p, hipStream_t stream) {
     }
 }
 
-template <int HD>
+template <typename KT, int HD>
 int launch_decode(const dlk_attention_params& p, hipStream_t stream) {
     int status = 0;
     switch (p.chunk / kWave) {
-    case 4: status = launch_decode_w<HD, 4>(p, stream); break;
-    case 8: status = launch_decode_w<HD, 8>(p, stream); break;
-    case 16: status = launch_decode_w<HD, 16>(p, stream); break;
+    case 4: status = launch_decode_w<KT, HD, 4>(p, stream); break;
+    case 8: status = launch_decode_w<KT, HD, 8>(p, stream); break;
+    case 16:
+        if constexpr (sizeof(KT) == 2) {
+            status = launch_decode_w<KT, HD, 16>(p, stream);
+            break;
+        }
+        return static_cast<int>(hipErrorInvalidValue);
     default: return static_cast<int>(hipErrorInvalidValue);
     }
     if (status != 0 || p.splits == 1 || p.partials_only) return status;
@@ -760,13 +821,13 @@ int launch_decode(const dlk_attention_params& p, hipStream_t stream) {
     return static_cast<int>(hipGetLastError());
 }
 
-/// The decode kernel serves one new position over bf16 K/V with HD 64 (G in {1, 2, 4, 8}) or 128 (G <= 4) and
-/// chunks of 4, 8 or 16 64-key tiles (one per wave).
+/// The decode kernel serves one new position over bf16 K/V with HD 64 (G in {1, 2, 4, 8}) or 128 (G <= 4), or
+/// over f32 K/V with HD 64, and chunks of 4, 8 or 16 64-key tiles (one per wave).
 int decode_chunk_max(int heads, int kv_heads, int hd, int kv_bf16) {
-    if (!kv_bf16 || kv_heads <= 0 || heads % kv_heads != 0 || (hd != 64 && hd != 128)) return 0;
+    if (kv_heads <= 0 || heads % kv_heads != 0 || (hd != 64 && hd != 128)) return 0;
     const int G = heads / kv_heads;
     if (!(G == 1 || G == 2 || G == 4 || (G == 8 && hd == 64))) return 0;
-    return decode_waves_max(hd, G) * kWave;
+    return decode_waves_max(hd, G, !kv_bf16) * kWave;
 }
 
 bool decode_path(const dlk_attention_params& p) {
@@ -808,9 +869,16 @@ extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stre
         (p.splits > 1 && (!p.partial_o || !p.partial_ml)) || (p.splits > 1 && p.chunk % 64 != 0))
         return static_cast<int>(hipErrorInvalidValue);
     if (p.L == 1 && dlk::stream_heads(p.H, p.KV, p.hd, p.kv_bf16) && p.chunk % 128 == 0 &&
-        (static_cast<int64_t>(p.B) * p.KV * p.splits * p.chunk >= DLK_STREAM_DECODE_KEYS || !dlk::decode_path(p)))
-        return p.hd == 64 ? dlk::launch_stream<64>(p, stream) : dlk::launch_stream<128>(p, stream);
-    if (dlk::decode_path(p)) return p.hd == 64 ? dlk::launch_decode<64>(p, stream) : dlk::launch_decode<128>(p, stream);
+        (static_cast<int64_t>(p.B) * p.KV * p.splits * p.chunk >= DLK_STREAM_DECODE_KEYS || !dlk::decode_path(p))) {
+        if (p.kv_bf16)
+            return p.hd == 64 ? dlk::launch_stream<uint16_t, 64>(p, stream) : dlk::launch_stream<uint16_t, 128>(p, stream);
+        return p.hd == 64 ? dlk::launch_stream<float, 64>(p, stream) : dlk::launch_stream<float, 128>(p, stream);
+    }
+    if (dlk::decode_path(p)) {
+        if (p.kv_bf16)
+            return p.hd == 64 ? dlk::launch_decode<uint16_t, 64>(p, stream) : dlk::launch_decode<uint16_t, 128>(p, stream);
+        return p.hd == 64 ? dlk::launch_decode<float, 64>(p, stream) : static_cast<int>(hipErrorInvalidValue);
+    }
     if (dlk_attention_prefill_eligible(&p)) return dlk_attention_prefill(&p, stream_handle);
     if (p.kv_bf16) {
         switch (p.hd) {

@@ -1,5 +1,5 @@
 // Causal grouped-query attention over a prefill chunk on the matrix cores (see dlk_attention_params in
-// kernels.h): bf16 K/V cache, head dim 64 or 128, one split.  Replaces, for L new positions, the query-blocked
+// kernels.h): bf16 or f32 K/V cache, head dim 64 or 128, one split.  Replaces, for L new positions, the query-blocked
 // grouped_block + attention_weights of the reference (src/ops/attention.cpp:59-95, 161-188): scores in f32,
 // causal rule key <= first + row (:52-57), softmax with the row maximum subtracted, P * V.
 //
@@ -15,7 +15,9 @@
 // operand of
 //   O^T[16 d][16 queries] += V^T[16 d][32 keys] * P^T     (A = V^T from the transposed LDS tile, in the key
 //                                                         order the lane holds; P split into hi + lo)
-// Two MFMAs per product (hi and lo) keep f32-level accuracy against the bf16 K and V.  The softmax runs in base 2
+// Two MFMAs per product (hi and lo) keep f32-level accuracy against the bf16 K and V.  An f32 cache is split the
+// same way when it is staged (K = Kh + Kl, V = Vh + Vl, each a bf16 plane in LDS), and each product takes three
+// MFMAs: Kh Qh + Kh Ql + Kl Qh (the Kl Ql term is below 2^-16 of the product) and likewise for V^T P^T.  The softmax runs in base 2
 // (log2 e folded into the score scale, one v_exp_f32 per score) and masks only the tiles that cross the causal
 // diagonal.  The row maxima cross the four lanes of a row with the in-register lane swaps (v_permlane32_swap,
 // v_permlane16_swap); the row sums come out of the matrix cores as one more output tile whose A operand is all
@@ -70,17 +72,31 @@ __device__ __forceinline__ void block_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int HD>
-__global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_attention_params p) {
+// bf16 hi and lo parts of four f32 values (round to nearest even twice: x - hi is exact in f32)
+__device__ __forceinline__ void split4(const u32x4 w, u32x2& hi, u32x2& lo) {
+    const f32x4 v = __builtin_bit_cast(f32x4, w);
+    const bf16x4 h = __builtin_convertvector(v, bf16x4);
+    const u32x2 hw = __builtin_bit_cast(u32x2, h);
+    const f32x4 back = {__uint_as_float(hw.x << 16), __uint_as_float(hw.x & 0xffff0000u),
+                        __uint_as_float(hw.y << 16), __uint_as_float(hw.y & 0xffff0000u)};
+    hi = hw;
+    lo = __builtin_bit_cast(u32x2, __builtin_convertvector(v - back, bf16x4));
+}
+
+template <typename KT, int HD>
+__global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_prefill(const dlk_attention_params p) {
+    constexpr bool F32 = sizeof(KT) == 4;
+    constexpr int PLANES = F32 ? 2 : 1;         // staged bf16 planes per tile: hi (+ lo for an f32 cache)
     constexpr int KS = HD / 32;                 // k steps of the score MFMA
     constexpr int DT = HD / 16;                 // 16-wide head-dim tiles of the output
     constexpr int KSTRIDE = HD + 8;             // bf16 per staged K row
     constexpr int VSTRIDE = kKeys + 8;          // bf16 per staged V^T row (one head-dim column)
-    constexpr int CHUNKS = kKeys * HD / 8;      // 16-byte pieces of one K (or V) tile
-    constexpr int LOADS = CHUNKS / kThreads;    // per thread
-    static_assert(CHUNKS % kThreads == 0 && LOADS % 2 == 0, "whole loads; V pieces come in key pairs");
-    __shared__ __attribute__((aligned(16))) uint16_t ks[2][kKeys * KSTRIDE];
-    __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * VSTRIDE];
+    constexpr int DPP = 16 / sizeof(KT);        // head-dim values per 16-byte piece
+    constexpr int NG = HD / DPP;                // pieces per K (or V) row
+    constexpr int LOADS = kKeys * NG / kThreads; // K pieces per thread per tile (and V pieces, in key pairs)
+    static_assert(kKeys * NG % kThreads == 0 && LOADS % 2 == 0, "whole loads; V pieces come in key pairs");
+    __shared__ __attribute__((aligned(16))) uint16_t ks[PLANES][2][kKeys * KSTRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[PLANES][2][HD * VSTRIDE];
 
     const int t = threadIdx.x, lane = t % kWave, q = lane / 16;
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
@@ -119,19 +135,20 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
         }
     }
 
-    // K staging: piece c = t + 256 i -> key c / (HD/8), head-dim group c % (HD/8), stored as loaded.  V staging:
-    // lane -> key pair kp = lane % 32 and head-dim group 2 wave + lane / 32 (+ 8 per pass): the two keys' pieces
-    // are transposed into 32-bit words (key pair) of the V^T rows, the 64 lanes of a wave hitting 64 banks.
-    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (static_cast<int64_t>(b) * p.KV + kvh) * p.capacity * HD;
-    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (static_cast<int64_t>(b) * p.KV + kvh) * p.capacity * HD;
+    // K staging: piece c = t + 256 i -> key c / NG, head-dim group c % NG, stored as loaded (an f32 piece split
+    // into its hi and lo planes).  V staging: lane -> key pair kp = lane % 32 and head-dim group 2 wave + lane / 32
+    // (+ 8 per pass): the two keys' pieces are transposed into 32-bit words (key pair) of the V^T rows, the 64
+    // lanes of a wave hitting 64 banks.
+    const KT* kbase = static_cast<const KT*>(p.k) + (static_cast<int64_t>(b) * p.KV + kvh) * p.capacity * HD;
+    const KT* vbase = static_cast<const KT*>(p.v) + (static_cast<int64_t>(b) * p.KV + kvh) * p.capacity * HD;
     const int kp = lane % 32;
     u32x4 kr[LOADS], vr[LOADS];
     auto load = [&](int tile) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            const int c = t + kThreads * i, key = c / (HD / 8), dg = c % (HD / 8);
+            const int c = t + kThreads * i, key = c / NG, dg = c % NG;
             const int row = min(tile * kKeys + key, S - 1); // in bounds; rows past the end are zeroed when staged
-            kr[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(row) * HD + 8 * dg);
+            kr[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(row) * HD + DPP * dg);
         }
 #pragma unroll
         for (int i = 0; i < LOADS / 2; ++i) {
@@ -139,16 +156,24 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const int row = min(tile * kKeys + 2 * kp + e, S - 1);
-                vr[2 * i + e] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(row) * HD + 8 * dg);
+                vr[2 * i + e] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(row) * HD + DPP * dg);
             }
         }
     };
     auto stage = [&](int tile, int buf) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            const int c = t + kThreads * i, key = c / (HD / 8), dg = c % (HD / 8);
+            const int c = t + kThreads * i, key = c / NG, dg = c % NG;
             const bool live = tile * kKeys + key < S;
-            *reinterpret_cast<u32x4*>(&ks[buf][key * KSTRIDE + 8 * dg]) = live ? kr[i] : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 w = live ? kr[i] : u32x4{0u, 0u, 0u, 0u};
+            if constexpr (F32) {
+                u32x2 hi, lo;
+                split4(w, hi, lo);
+                *reinterpret_cast<u32x2*>(&ks[0][buf][key * KSTRIDE + DPP * dg]) = hi;
+                *reinterpret_cast<u32x2*>(&ks[PLANES - 1][buf][key * KSTRIDE + DPP * dg]) = lo;
+            } else {
+                *reinterpret_cast<u32x4*>(&ks[0][buf][key * KSTRIDE + DPP * dg]) = w;
+            }
         }
 #pragma unroll
         for (int i = 0; i < LOADS / 2; ++i) {
@@ -156,12 +181,30 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
             const bool live0 = tile * kKeys + 2 * kp < S, live1 = tile * kKeys + 2 * kp + 1 < S;
             const u32x4 v0 = live0 ? vr[2 * i] : u32x4{0u, 0u, 0u, 0u};
             const u32x4 v1 = live1 ? vr[2 * i + 1] : u32x4{0u, 0u, 0u, 0u};
-            const uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w}, c[4] = {v1.x, v1.y, v1.z, v1.w};
-            uint32_t* col = reinterpret_cast<uint32_t*>(&vt[buf][8 * dg * VSTRIDE + 2 * kp]);
+            if constexpr (F32) {
+                // key 2 kp's hi (lo) values in the low halves, key 2 kp + 1's in the high halves
+                u32x2 h0, l0, h1, l1;
+                split4(v0, h0, l0);
+                split4(v1, h1, l1);
+                const uint32_t h[4] = {h0.x & 0xffffu, h0.x >> 16, h0.y & 0xffffu, h0.y >> 16};
+                const uint32_t hn[4] = {h1.x << 16, h1.x & 0xffff0000u, h1.y << 16, h1.y & 0xffff0000u};
+                const uint32_t l[4] = {l0.x & 0xffffu, l0.x >> 16, l0.y & 0xffffu, l0.y >> 16};
+                const uint32_t ln[4] = {l1.x << 16, l1.x & 0xffff0000u, l1.y << 16, l1.y & 0xffff0000u};
+                uint32_t* col_h = reinterpret_cast<uint32_t*>(&vt[0][buf][DPP * dg * VSTRIDE + 2 * kp]);
+                uint32_t* col_l = reinterpret_cast<uint32_t*>(&vt[PLANES - 1][buf][DPP * dg * VSTRIDE + 2 * kp]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                col[(2 * e) * (VSTRIDE / 2)] = (a[e] & 0xffffu) | (c[e] << 16);        // head-dim 8 dg + 2 e
-                col[(2 * e + 1) * (VSTRIDE / 2)] = (a[e] >> 16) | (c[e] & 0xffff0000u); // head-dim 8 dg + 2 e + 1
+                for (int e = 0; e < 4; ++e) {
+                    col_h[e * (VSTRIDE / 2)] = h[e] | hn[e]; // head-dim 4 dg + e
+                    col_l[e * (VSTRIDE / 2)] = l[e] | ln[e];
+                }
+            } else {
+                const uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w}, c[4] = {v1.x, v1.y, v1.z, v1.w};
+                uint32_t* col = reinterpret_cast<uint32_t*>(&vt[0][buf][DPP * dg * VSTRIDE + 2 * kp]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    col[(2 * e) * (VSTRIDE / 2)] = (a[e] & 0xffffu) | (c[e] << 16);        // head-dim 8 dg + 2 e
+                    col[(2 * e + 1) * (VSTRIDE / 2)] = (a[e] >> 16) | (c[e] & 0xffff0000u); // head-dim 8 dg + 2 e + 1
+                }
             }
         }
     };
@@ -187,11 +230,14 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
         // scores: s[i][qt] = S[keys 64 tile + 16 i + 4 q + j][query row (qt, lane % 16)]
         // the K fragments are read ahead so that the reads overlap: the whole tile at head dim 64, one 16-key
         // block at a time at 128 (whose registers would not hold the whole tile)
-        bf16x8 kf[4][KS];
+        bf16x8 kf[4][KS], kl[4][KS];
         auto read_k = [&](int i) {
 #pragma unroll
-            for (int st = 0; st < KS; ++st)
-                kf[i][st] = *reinterpret_cast<const bf16x8*>(&ks[buf][(16 * i + lane % 16) * KSTRIDE + 32 * st + 8 * q]);
+            for (int st = 0; st < KS; ++st) {
+                const int at = (16 * i + lane % 16) * KSTRIDE + 32 * st + 8 * q;
+                kf[i][st] = *reinterpret_cast<const bf16x8*>(&ks[0][buf][at]);
+                if constexpr (F32) kl[i][st] = *reinterpret_cast<const bf16x8*>(&ks[PLANES - 1][buf][at]);
+            }
         };
         if constexpr (HD == 64) {
 #pragma unroll
@@ -209,6 +255,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
                 for (int qt = 0; qt < 2; ++qt) {
                     s[i][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i][st], qh[qt][st], s[i][qt], 0, 0, 0);
                     s[i][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i][st], ql[qt][st], s[i][qt], 0, 0, 0);
+                    if constexpr (F32)
+                        s[i][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl[i][st], qh[qt][st], s[i][qt], 0, 0, 0);
                 }
             }
         }
@@ -262,14 +310,22 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
         for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const uint16_t* col = &vt[buf][(16 * dt + lane % 16) * VSTRIDE + 32 * u + 4 * q];
-                const u32x2 lo4 = *reinterpret_cast<const u32x2*>(col);
-                const u32x2 hi4 = *reinterpret_cast<const u32x2*>(col + 16);
+                const int at = (16 * dt + lane % 16) * VSTRIDE + 32 * u + 4 * q;
+                const u32x2 lo4 = *reinterpret_cast<const u32x2*>(&vt[0][buf][at]);
+                const u32x2 hi4 = *reinterpret_cast<const u32x2*>(&vt[0][buf][at + 16]);
                 const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
+                bf16x8 al;
+                if constexpr (F32) {
+                    const u32x2 llo4 = *reinterpret_cast<const u32x2*>(&vt[PLANES - 1][buf][at]);
+                    const u32x2 lhi4 = *reinterpret_cast<const u32x2*>(&vt[PLANES - 1][buf][at + 16]);
+                    al = __builtin_bit_cast(bf16x8, u32x4{llo4.x, llo4.y, lhi4.x, lhi4.y});
+                }
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) {
                     o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[u][qt], o[qt][dt], 0, 0, 0);
                     o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[u][qt], o[qt][dt], 0, 0, 0);
+                    if constexpr (F32)
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ph[u][qt], o[qt][dt], 0, 0, 0);
                 }
             }
         }
@@ -302,7 +358,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_prefill(const dlk_atten
 /* Whether dlk_attention takes the matrix-core prefill kernel for these parameters. */
 extern "C" int dlk_attention_prefill_eligible(const dlk_attention_params* p) {
     const int G = p->KV > 0 ? p->H / p->KV : 0;
-    return p->kv_bf16 && (p->hd == 64 || p->hd == 128) && p->L >= 16 && G > 0 && dlk::kRows % G == 0 &&
+    return p->causal && (p->hd == 64 || p->hd == 128) && p->L >= 16 && G > 0 && dlk::kRows % G == 0 &&
            p->splits == 1 && p->ldq % 4 == 0 && p->ldo % 4 == 0;
 }
 
@@ -312,9 +368,12 @@ extern "C" int dlk_attention_prefill(const dlk_attention_params* params, dlh_str
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
     const int per_head = dlk::kRows / (p.H / p.KV);
     const dim3 grid((p.L + per_head - 1) / per_head, p.B * p.KV);
-    if (p.hd == 64)
-        hipLaunchKernelGGL(dlk::attention_prefill<64>, grid, dim3(dlk::kThreads), 0, stream, p);
-    else
-        hipLaunchKernelGGL(dlk::attention_prefill<128>, grid, dim3(dlk::kThreads), 0, stream, p);
+    if (p.kv_bf16) {
+        if (p.hd == 64) hipLaunchKernelGGL((dlk::attention_prefill<uint16_t, 64>), grid, dim3(dlk::kThreads), 0, stream, p);
+        else hipLaunchKernelGGL((dlk::attention_prefill<uint16_t, 128>), grid, dim3(dlk::kThreads), 0, stream, p);
+    } else {
+        if (p.hd == 64) hipLaunchKernelGGL((dlk::attention_prefill<float, 64>), grid, dim3(dlk::kThreads), 0, stream, p);
+        else hipLaunchKernelGGL((dlk::attention_prefill<float, 128>), grid, dim3(dlk::kThreads), 0, stream, p);
+    }
     return static_cast<int>(hipGetLastError());
 }

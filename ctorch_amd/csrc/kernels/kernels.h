@@ -132,7 +132,7 @@ typedef struct dlk_attention_params {
     int partials_only;       /* splits > 1: leave the merge of the partials to the caller (no combine launch) */
 } dlk_attention_params;
 
-/* Keys per split of the one-position decode kernel (bf16 K/V, L = 1): 256, 512 or 1024 (64 per wave). */
+/* Keys per split of the one-position decode kernel (L = 1): 256, 512 or 1024 (64 per wave; f32 K/V at most 512). */
 #define DLK_DECODE_CHUNK_MAX 1024
 /* The widest decode chunk for this head layout (0 when the decode kernel does not apply). */
 int dlk_attention_decode_chunk(int heads, int kv_heads, int head_dim, int kv_bf16);
@@ -140,13 +140,13 @@ int dlk_attention_decode_chunk(int heads, int kv_heads, int head_dim, int kv_bf1
    kernel when it serves the head layout: four waves per work-group, each streaming chunk / 4 keys (chunk a
    multiple of 128). */
 #define DLK_STREAM_DECODE_KEYS 32768
-/* 1 when the streaming decode kernel serves this head layout (bf16 K/V, head dim 64 or 128, H/KV <= 4). */
+/* 1 when the streaming decode kernel serves this head layout (bf16 or f32 K/V, head dim 64 or 128, H/KV <= 4). */
 int dlk_attention_stream_decode(int heads, int kv_heads, int head_dim, int kv_bf16);
 
 
 int dlk_attention(const dlk_attention_params* p, dlh_stream stream);
-/* The matrix-core causal prefill kernel (attention_prefill.hip), which dlk_attention takes for bf16 K/V, head
-   dim 64 or 128, L >= 16 new positions, one split and H/KV dividing 128. */
+/* The matrix-core causal prefill kernel (attention_prefill.hip), which dlk_attention takes for causal launches
+   over bf16 or f32 K/V, head dim 64 or 128, L >= 16 new positions, one split and H/KV dividing 128. */
 int dlk_attention_prefill_eligible(const dlk_attention_params* p);
 int dlk_attention_prefill(const dlk_attention_params* p, dlh_stream stream);
 

@@ -9,9 +9,7 @@ namespace dl::detail {
 using nn::KVCache;
 using nn::TransformerDecoderLayer;
 
-DType cache_dtype(const TransformerDecoderLayer& layer) {
-    return layer.attention().query().weight().dtype() == DType::bf16 ? DType::bf16 : DType::f32;
-}
+DType cache_dtype(const TransformerDecoderLayer& layer) { return layer.attention().cache_dtype(); }
 
 void DecodeWorkspace::ensure(const TransformerDecoderLayer& layer, Index n, Index heads_total, Index hidden_features,
                              int splits, Device device) {

@@ -46,7 +46,8 @@ void decode_layer(const nn::TransformerDecoderLayer& layer, const float* x_in, f
                   nn::KVCache& cache, DecodeWorkspace& ws, int splits, int chunk, GpuContext& context,
                   LaunchObserver* observer = nullptr);
 
-/// The KV storage dtype the fused path uses for a layer: bf16 when the projections are bf16, else f32.
+/// The KV storage dtype the fused path reserves for a layer (its attention's cache dtype: f32 unless bf16 was
+/// chosen).
 DType cache_dtype(const nn::TransformerDecoderLayer& layer);
 
 } // namespace dl::detail

@@ -179,6 +179,11 @@ void GroupedQueryAttention::attach_lora(Index rank, double alpha, bool query, bo
         value_adapter_ = add_module<LoRAAdapter>("value_adapter", dimensions_, kv_heads_ * head_dim(), rank, alpha, options);
 }
 
+void GroupedQueryAttention::set_cache_dtype(DType dtype) {
+    if (dtype != DType::f32 && dtype != DType::bf16) throw std::invalid_argument("KV cache dtype must be f32 or bf16");
+    cache_dtype_ = dtype;
+}
+
 Tensor GroupedQueryAttention::forward(const Tensor& input) { return run(input, nullptr); }
 
 Tensor GroupedQueryAttention::decode(const Tensor& input, KVCache& cache) { return run(input, &cache); }
@@ -199,7 +204,7 @@ Tensor GroupedQueryAttention::run(const Tensor& input, KVCache* cache) {
     Tensor x = contiguous_f32(input);
     Tensor out = empty_tensor({B, L, d}, DType::f32, input.device());
     const Index hd = head_dim();
-    const DType kv_dtype = query_->weight().dtype() == DType::bf16 ? DType::bf16 : DType::f32;
+    const DType kv_dtype = cache_dtype_;
     target.reserve(B, kv_heads_, hd, kv_dtype, input.device());
     const Index rows = B * L;
     Tensor q = empty_tensor({rows, heads_ * hd}, DType::f32, input.device());
@@ -332,6 +337,12 @@ void TransformerDecoder::attach_lora(Index rank, double alpha, bool query, bool 
     for (auto& layer : layers_) layer->attention().attach_lora(rank, alpha, query, value);
 }
 
+void TransformerDecoder::set_cache_dtype(DType dtype) {
+    for (auto& layer : layers_) layer->attention().set_cache_dtype(dtype);
+}
+
+DType TransformerDecoder::cache_dtype() const { return layers_.front()->attention().cache_dtype(); }
+
 Tensor TransformerDecoder::forward(const Tensor& input) {
     std::vector<KVCache> cache;
     for (std::size_t i = 0; i < layers_.size(); ++i) cache.emplace_back(std::max<Index>(1, input.size(1)));
@@ -369,10 +380,10 @@ Tensor TransformerDecoder::decode(const Tensor& input, std::span<KVCache> cache)
         int splits = 1, chunk = 64;
         const auto& front = layers_.front()->attention();
         attention_split(B, front.heads(), front.kv_heads(), front.head_dim(),
-                        cache_dtype(*layers_.front()) == DType::bf16, L, prefix + L, splits, chunk);
+                        detail::cache_dtype(*layers_.front()) == DType::bf16, L, prefix + L, splits, chunk);
         for (std::size_t i = 0; i < layers_.size(); ++i) {
             cache[i].reserve(B, layers_[i]->attention().kv_heads(), layers_[i]->attention().head_dim(),
-                             cache_dtype(*layers_[i]), input.device());
+                             detail::cache_dtype(*layers_[i]), input.device());
             decode_layer(*layers_[i], xd, xd, B, L, cache[i], ws, splits, chunk, context);
         }
         Tensor out = empty_tensor({B, L, d}, DType::f32, input.device());

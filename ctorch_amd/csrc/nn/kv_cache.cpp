@@ -42,21 +42,28 @@ void KVCache::append(const Tensor& key, const Tensor& value) {
     const auto count = key.size(-2);
     if (count != value.size(-2) || count > capacity_ - length_)
         throw std::invalid_argument("KV cache append exceeds capacity or has unequal key/value lengths");
-    if (!key_) {
-        Shape shape = key.shape();
+    // as in the reference: key and value storage each take their input's shape (capacity rows), dtype and device
+    // on the first append, and a later append that differs in any of them throws
+    auto storage_shape = [&](const Tensor& input) {
+        Shape shape = input.shape();
         shape[shape.size() - 2] = capacity_;
-        key_ = empty_tensor(shape, key.dtype(), key.device());
-        value_ = empty_tensor(shape, key.dtype(), key.device());
+        return shape;
+    };
+    if (!key_) {
+        if (!(key.device() == value.device())) throw std::invalid_argument("KV cache shape, dtype or device changed");
+        key_ = empty_tensor(storage_shape(key), key.dtype(), key.device());
+        value_ = empty_tensor(storage_shape(value), value.dtype(), value.device());
         if (key.device().type == DeviceType::gpu) position_ = empty_tensor({1}, DType::i64, key.device());
     } else {
-        Shape shape = key.shape();
-        shape[shape.size() - 2] = capacity_;
-        if (key_->shape() != shape || !(key_->device() == key.device()))
+        auto differs = [&](const Tensor& input, const Tensor& storage) {
+            return storage.shape() != storage_shape(input) || storage.dtype() != input.dtype() ||
+                   !(storage.device() == input.device());
+        };
+        if (differs(key, *key_) || differs(value, *value_))
             throw std::invalid_argument("KV cache shape, dtype or device changed");
     }
-    // values are stored in the cache's dtype (bf16 storage for bf16 models)
-    copy_into(key_->narrow(-2, length_, count), key.to(key_->device()));
-    copy_into(value_->narrow(-2, length_, count), value.to(value_->device()));
+    copy_into(key_->narrow(-2, length_, count), key);
+    copy_into(value_->narrow(-2, length_, count), value);
     length_ += count;
     sync_position();
 }

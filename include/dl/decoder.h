@@ -3,7 +3,8 @@
 // RotaryEmbedding, KVCache, GroupedQueryAttention, TransformerDecoderLayer, TransformerDecoder) with the same
 // constructor arguments, state names and decode semantics.  Additive extensions, each documented where it
 // is declared: a RoPE base for the attention/decoder (the reference hard-codes 10000), unmerged LoRA
-// adapters attached to the query/value projections, and a KV storage dtype (bf16 for bf16 models).
+// adapters attached to the query/value projections, and an opt-in bf16 KV storage dtype (the default, as in the
+// reference, stores K/V in the f32 dtype the projections produce).
 
 #include "dl/nn.h"
 
@@ -72,9 +73,10 @@ private:
 };
 
 /// Per-request K/V store appended along the second-to-last axis.  Storage [B, KV, capacity, D] is allocated
-/// once by the first append (which also fixes the other dimensions, dtype and device); clear/truncate reuse
-/// it and key()/value() are views of it.  On the GPU the cache also keeps its length in device memory so
-/// that a captured token step reads the current position without host arguments.
+/// once by the first append (which also fixes the other dimensions, dtype and device: a later append of another
+/// shape, dtype or device throws); clear/truncate reuse it and key()/value() are views of it.  On the GPU the
+/// cache also keeps its length in device memory so that a captured token step reads the current position
+/// without host arguments.
 class DL_API KVCache {
 public:
     explicit KVCache(Index capacity);
@@ -119,6 +121,12 @@ public:
 
     /// Extension: attaches unmerged rank-`rank` adapters to the query and/or value projection.
     void attach_lora(Index rank, double alpha, bool query = true, bool value = true);
+    /// Extension: the dtype of the K/V storage this module's decode reserves.  The default is f32, the dtype of
+    /// the projections' output, which the reference's cache takes from its first append
+    /// (src/nn/kv_cache.cpp:16-21); bf16 halves the cache bytes of long-context decode at the cost of rounding
+    /// every stored key and value.  Set it before the first decode into a cache.
+    void set_cache_dtype(DType dtype);
+    DType cache_dtype() const { return cache_dtype_; }
 
     Index dimensions() const { return dimensions_; }
     Index heads() const { return heads_; }
@@ -135,6 +143,7 @@ public:
 private:
     Tensor run(const Tensor& input, KVCache* cache);
     Index dimensions_, heads_, kv_heads_;
+    DType cache_dtype_ = DType::f32;
     std::shared_ptr<Linear> query_, key_, value_, output_;
     std::shared_ptr<RotaryEmbedding> rotary_;
     std::shared_ptr<LoRAAdapter> query_adapter_, value_adapter_;
@@ -176,6 +185,10 @@ public:
 
     /// Extension: attaches unmerged adapters to every layer's query/value projections.
     void attach_lora(Index rank, double alpha, bool query = true, bool value = true);
+    /// Extension: every layer's K/V storage dtype (GroupedQueryAttention::set_cache_dtype): f32 by default,
+    /// bf16 as an opt-in for long-context decode.
+    void set_cache_dtype(DType dtype);
+    DType cache_dtype() const;
 
     Index context() const { return context_; }
     TransformerDecoderLayer& layer(Index i) { return *layers_.at(static_cast<std::size_t>(i)); }

@@ -55,6 +55,13 @@ DL_API dl_status dl_transformer_decoder_create_with_base(int64_t layers, int64_t
  * layer{i}.attention.{query,value}_adapter.{down,up}.weight. */
 DL_API dl_status dl_transformer_decoder_attach_lora(dl_module* decoder, int64_t rank, double alpha,
     int32_t query, int32_t value);
+/* Extension (no reference counterpart): the dtype of the K/V storage every layer's decode reserves.  DL_F32, the
+ * default, is the reference's: its KVCache takes the dtype of the appended keys (src/nn/kv_cache.cpp:16-21),
+ * which is linear's f32 output (src/ops/matmul.cpp:35-67).  DL_BF16 is an opt-in that halves the cache bytes of
+ * long-context decode and rounds every stored key and value to bf16.  Set it before the first decode into a
+ * cache: a cache already holding storage of the other dtype is refused on the next decode. */
+DL_API dl_status dl_transformer_decoder_set_cache_dtype(dl_module* decoder, dl_dtype dtype);
+DL_API dl_status dl_transformer_decoder_cache_dtype(const dl_module* decoder, dl_dtype* dtype);
 /* The ONNX decoder's cache wire format (reference extensions/onnx/src/decoder.cpp:64-69, docs/onnx.md:68-113):
  * per layer i, past_key_i / past_value_i as f32 [batch, kv_heads, length, head_dim].  cache_state writes the
  * cache under those names (ready to feed an ONNX Runtime session as its next past_* inputs).  cache_load_state

@@ -306,10 +306,12 @@ def synthesize_weights(cfg: ModelConfig, root=(1234, 0), scale: float = 0.02) ->
 class OracleLM:
     """Embedding -> TransformerDecoder -> untied head, evaluated by the CPU oracle."""
 
-    def __init__(self, cfg: ModelConfig, weights: dict[str, np.ndarray], kv_bf16: bool | None = None):
+    def __init__(self, cfg: ModelConfig, weights: dict[str, np.ndarray], kv_bf16: bool = False):
+        """kv_bf16=False keeps the reference's f32 cache (src/nn/kv_cache.cpp:16-21: the cache takes the dtype
+        of linear's f32 output); True rounds every appended key and value to bf16, the product's opt-in."""
         self.cfg = cfg
         self.w = {k: np.ascontiguousarray(v) for k, v in weights.items()}
-        self.kv_bf16 = (cfg.dtype == "bf16") if kv_bf16 is None else kv_bf16
+        self.kv_bf16 = bool(kv_bf16)
         hd = cfg.head_dim
         self.tables = []
         for i in range(cfg.layers):

@@ -94,7 +94,7 @@ typedef struct orc_config {
     int64_t vocab, layers, dimensions, heads, kv_heads, hidden, context;
     double rope_base, epsilon;
     int wdtype;      /* ORC_F32 or ORC_BF16 for every projection / embedding / head */
-    int kv_bf16;     /* 1: K/V are rounded to bf16 on append (the build's storage choice) */
+    int kv_bf16;     /* 0: f32 K/V as the reference stores them; 1: rounded to bf16 on append (the bf16 cache opt-in) */
     int64_t lora_rank; double lora_alpha; /* rank 0: no adapters */
 } orc_config;
 

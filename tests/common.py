@@ -13,12 +13,15 @@ import oracle
 
 
 class GpuLM:
-    def __init__(self, cfg: oracle.ModelConfig, weights: dict[str, np.ndarray]):
+    """kv_dtype: the decoder's K/V storage (None: the default f32, as the reference stores it; ct.BF16: the
+    opt-in)."""
+
+    def __init__(self, cfg: oracle.ModelConfig, weights: dict[str, np.ndarray], kv_dtype=None):
         dtype = ct.BF16 if cfg.dtype == "bf16" else ct.F32
         gpu = ct.device("gpu")
         self.cfg = cfg
         self.decoder = ct.transformer_decoder(cfg.layers, cfg.dimensions, cfg.heads, cfg.kv_heads, cfg.hidden,
-                                              cfg.context, dtype, gpu, cfg.rope_base)
+                                              cfg.context, dtype, gpu, cfg.rope_base, kv_dtype=kv_dtype)
         if cfg.lora_rank:
             ct.check(ct.lib().dl_transformer_decoder_attach_lora(self.decoder.handle, cfg.lora_rank, cfg.lora_alpha,
                                                                  1, 1))
@@ -45,9 +48,26 @@ class GpuLM:
         return self.lm.logits(ids, cache)
 
 
-def build_pair(cfg: oracle.ModelConfig, root=(1234, 0), scale: float = 0.02, weights=None):
+def build_pair(cfg: oracle.ModelConfig, root=(1234, 0), scale: float = 0.02, weights=None, kv_dtype=None):
+    """The oracle with the reference's f32 K/V cache, and the GPU model (f32 K/V unless kv_dtype is ct.BF16)."""
     weights = weights if weights is not None else oracle.synthesize_weights(cfg, root, scale)
-    return oracle.OracleLM(cfg, weights), GpuLM(cfg, weights)
+    return oracle.OracleLM(cfg, weights, kv_bf16=False), GpuLM(cfg, weights, kv_dtype)
+
+
+KV_DTYPES = {"f32": None, "bf16": ct.BF16}
+
+
+def seed_prefix(ref_cache, gpu_cache, layer, keys, values, kv_dtype):
+    """Writes a seeded prefix into both caches through KVCache::append: bf16-exact values, stored on the GPU in
+    the cache's dtype (f32 by default, bf16 for the opt-in) and as f32 in the oracle's cache."""
+    kb, vb = oracle.bf16_encode(keys), oracle.bf16_encode(values)
+    kf, vf = oracle.bf16_decode(kb), oracle.bf16_decode(vb)
+    gpu = ct.device("gpu")
+    if kv_dtype == ct.BF16:
+        gpu_cache.append(layer, ct.Tensor.from_numpy(kb, ct.BF16, gpu), ct.Tensor.from_numpy(vb, ct.BF16, gpu))
+    else:
+        gpu_cache.append(layer, ct.Tensor.from_numpy(kf, ct.F32, gpu), ct.Tensor.from_numpy(vf, ct.F32, gpu))
+    ref_cache.fill(layer, keys.shape[2], kf, vf)
 
 
 def rel_err(got: np.ndarray, want: np.ndarray) -> float:

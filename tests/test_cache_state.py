@@ -24,8 +24,12 @@ def bf16_round(x):
 
 def test_cache_state_round_trips_in_the_decoder_cache_dtype():
     rng = np.random.default_rng(5)
-    for dtype, rounding in ((ct.BF16, bf16_round), (ct.F32, lambda x: x)):
-        dec = ct.transformer_decoder(2, 64, 4, 2, 96, 24, dtype, ct.device("cpu"))
+    # the default cache dtype is f32 for f32 and bf16 models alike (the reference's cache takes linear's f32
+    # output dtype, src/nn/kv_cache.cpp:16-21); bf16 storage is an explicit opt-in and rounds the imported values
+    for dtype, kv_dtype, rounding in ((ct.BF16, None, lambda x: x), (ct.BF16, ct.BF16, bf16_round),
+                                      (ct.F32, None, lambda x: x), (ct.F32, ct.BF16, bf16_round)):
+        dec = ct.transformer_decoder(2, 64, 4, 2, 96, 24, dtype, ct.device("cpu"), kv_dtype=kv_dtype)
+        assert ct.cache_dtype(dec) == (ct.F32 if kv_dtype is None else kv_dtype)
         cache = ct.DecoderCache(dec)
         past = past_state(rng, 2, 3, 2, 5, 16)
         cache.load_state(dec, past)

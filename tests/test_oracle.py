@@ -300,8 +300,9 @@ def test_decoder_chunked_equals_full_and_rollback():
     assert small.lengths == [1, 1]
 
 
-def _torch_decoder(cfg, w, ids):
-    """Float64 restatement with torch primitives (an independent check of structure and indices)."""
+def _torch_decoder(cfg, w, ids, kv_round=None):
+    """Float64 restatement with torch primitives (an independent check of structure and indices).  kv_round, if
+    given, is applied to the rotated keys and the values before attention (the bf16 cache opt-in)."""
     d, H, KV, hd = cfg.dimensions, cfg.heads, cfg.kv_heads, cfg.head_dim
     dec = (lambda a: torch.from_numpy(oracle.bf16_decode(a)).double()) if cfg.dtype == "bf16" else \
         (lambda a: torch.from_numpy(np.asarray(a, np.float32)).double())
@@ -324,6 +325,8 @@ def _torch_decoder(cfg, w, ids):
         q = rope((h @ dec(w[p + "attention.query.weight"]).T).reshape(B, L, H, hd)).transpose(1, 2)
         k = rope((h @ dec(w[p + "attention.key.weight"]).T).reshape(B, L, KV, hd)).transpose(1, 2)
         v = (h @ dec(w[p + "attention.value.weight"]).T).reshape(B, L, KV, hd).transpose(1, 2)
+        if kv_round is not None:
+            k, v = kv_round(k), kv_round(v)
         k = k.repeat_interleave(H // KV, 1)
         v = v.repeat_interleave(H // KV, 1)
         a = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
@@ -345,6 +348,37 @@ def test_decoder_lm_vs_torch_float64(dtype):
     got = lm.logits(ids, lm.make_cache(2))
     ref = _torch_decoder(cfg, w, ids)
     assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) < 1e-5
+
+
+def test_bf16_cache_mode_vs_torch_float64_with_rounded_keys_and_values():
+    # kv_bf16=True (the product's bf16 cache opt-in) rounds every stored key and value to bf16 (RNE) and reads
+    # them back; the restatement rounds its own float64 K/V through torch's bf16 conversion.  The reference's f32
+    # cache (kv_bf16=False) differs from that restatement by far more than the bound, and so would a mode that
+    # rounded only K or only V.
+    cfg = _tiny("bf16")
+    w = oracle.synthesize_weights(cfg, (22, 0), scale=0.3)
+    ids = oracle.random_ids((6, 0), 2 * 9, cfg.vocab).reshape(2, 9)
+    to_bf16 = lambda t: t.to(torch.bfloat16).double()
+    rounded = _torch_decoder(cfg, w, ids, kv_round=to_bf16)
+    bound = 2e-5 * np.max(np.abs(rounded))
+    got = oracle.OracleLM(cfg, w, kv_bf16=True)
+    gap = np.max(np.abs(got.logits(ids, got.make_cache(2)) - rounded))
+    assert gap < bound, gap
+    plain = oracle.OracleLM(cfg, w, kv_bf16=False)
+    assert np.max(np.abs(plain.logits(ids, plain.make_cache(2)) - rounded)) > 10 * bound
+    for only in ("k", "v"):
+        half = _torch_decoder_partial_round(cfg, w, ids, only)
+        assert np.max(np.abs(half - rounded)) > 10 * bound, only
+
+
+def _torch_decoder_partial_round(cfg, w, ids, only):
+    calls = {"n": 0}
+
+    def round_one(t):  # called for k then v in every layer: round only the chosen one
+        which = "k" if calls["n"] % 2 == 0 else "v"
+        calls["n"] += 1
+        return t.to(torch.bfloat16).double() if which == only else t
+    return _torch_decoder(cfg, w, ids, kv_round=round_one)
 
 
 def test_generate_greedy_is_consistent_with_stepwise_logits():
