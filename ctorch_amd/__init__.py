@@ -97,6 +97,11 @@ SIGNATURES = {
     "dl_gpu_memory_set_release_threshold": (_st, [_i32, C.c_uint64]),
     "dl_gpu_memory_reset_peak_stats": (_st, [_i32]),
     "dl_gpu_memory_release_unused": (_st, [_i32]),
+    "dl_cuda_memory_get_stats": (_st, [_i32, C.POINTER(MemoryStats)]),
+    "dl_cuda_memory_set_release_threshold": (_st, [_i32, C.c_uint64]),
+    "dl_cuda_memory_reset_peak_stats": (_st, [_i32]),
+    "dl_cuda_memory_release_unused": (_st, [_i32]),
+    "dl_grad_enabled": (_i32, []),
     "dl_random_fold_in": (RandomKey, [RandomKey, C.c_uint64]),
     "dl_random_split": (None, [RandomKey, C.c_size_t, C.POINTER(RandomKey)]),
     "dl_uniform_with_key": (_st, [RandomKey, Shape, _f64, _f64, TensorOptions, _pp]),

@@ -2,6 +2,7 @@
 // 465,581-586, src/api/statistics.cpp:16-22).
 #include "api/common.h"
 #include "core/tensor_impl.h"
+#include "dl/autograd.h"
 #include "dl/gpu.h"
 
 #include <cstring>
@@ -163,6 +164,17 @@ dl_status dl_gpu_memory_reset_peak_stats(int32_t device) {
 dl_status dl_gpu_memory_release_unused(int32_t device) {
     return invoke([&] { dl::gpu::release_unused_memory(device); });
 }
+
+dl_status dl_cuda_memory_get_stats(int32_t device, dl_cuda_memory_stats* output) {
+    return dl_gpu_memory_get_stats(device, output);
+}
+dl_status dl_cuda_memory_set_release_threshold(int32_t device, uint64_t bytes) {
+    return dl_gpu_memory_set_release_threshold(device, bytes);
+}
+dl_status dl_cuda_memory_reset_peak_stats(int32_t device) { return dl_gpu_memory_reset_peak_stats(device); }
+dl_status dl_cuda_memory_release_unused(int32_t device) { return dl_gpu_memory_release_unused(device); }
+
+int32_t dl_grad_enabled(void) { return dl::is_grad_enabled() ? 1 : 0; }
 
 dl_random_key dl_random_fold_in(dl_random_key key, uint64_t label) { return convert(dl::fold_in(convert(key), label)); }
 

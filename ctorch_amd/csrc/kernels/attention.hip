@@ -747,6 +747,80 @@ __global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2)
     }
 }
 
+// ------------------------------------------------------------------------------------------ small heads
+// Head sizes below 16 (the reference's tiny test decoders: tests/c_api.c:31 builds one with head size 2).  Not a hot
+// path: one wave per (query row, key split); lane = key within each 64-key step, the scores and the weighted V
+// columns reduced over the wave, online softmax across the steps.  Writes the output, or (o, max, sum) partials
+// for attention_combine when the keys are split.
+template <typename KT, int HD>
+__global__ __launch_bounds__(kWave) void attention_small(const dlk_attention_params p) {
+    const int lane = threadIdx.x;
+    const int64_t prow = blockIdx.x; // (b * H + h) * L + l
+    const int split = blockIdx.y;
+    const int l = static_cast<int>(prow % p.L), h = static_cast<int>((prow / p.L) % p.H);
+    const int b = static_cast<int>(prow / (static_cast<int64_t>(p.L) * p.H));
+    const int kvh = h / (p.H / p.KV);
+    const int64_t first = p.position ? *p.position : p.first_host;
+    const int64_t S = first + p.L;
+    const int64_t visible = p.causal ? min(S, first + l + 1) : S;
+    const int64_t k_begin = static_cast<int64_t>(split) * p.chunk;
+    const int64_t k_end = min(visible, k_begin + p.chunk);
+    const float* qrow = p.q + (static_cast<int64_t>(b) * p.L + l) * p.ldq + static_cast<int64_t>(h) * HD;
+    float q[HD];
+#pragma unroll
+    for (int d = 0; d < HD; ++d) q[d] = qrow[d] * p.scale;
+    const size_t head = (static_cast<size_t>(b) * p.KV + kvh) * p.capacity;
+    const KT* kbase = static_cast<const KT*>(p.k) + head * HD;
+    const KT* vbase = static_cast<const KT*>(p.v) + head * HD;
+    auto value = [](const KT* row, int d) {
+        if constexpr (sizeof(KT) == 2) return bf16_to_f32(reinterpret_cast<const uint16_t*>(row)[d]);
+        else return static_cast<float>(row[d]);
+    };
+    float m = -INFINITY, total = 0.0f, o[HD];
+#pragma unroll
+    for (int d = 0; d < HD; ++d) o[d] = 0.0f;
+    for (int64_t k0 = k_begin; k0 < k_end; k0 += kWave) {
+        const int64_t key = k0 + lane;
+        const bool live = key < k_end;
+        float s = -INFINITY;
+        if (live) {
+            s = 0.0f;
+#pragma unroll
+            for (int d = 0; d < HD; ++d) s += q[d] * value(kbase + key * HD, d);
+        }
+        const float m_new = fmaxf(m, wave_max(s)); // finite: every step holds at least one live key
+        const float alpha = m == -INFINITY ? 0.0f : expf(m - m_new);
+        const float pr = live ? expf(s - m_new) : 0.0f;
+        total = total * alpha + wave_sum(pr);
+#pragma unroll
+        for (int d = 0; d < HD; ++d) o[d] = o[d] * alpha + wave_sum(live ? pr * value(vbase + key * HD, d) : 0.0f);
+        m = m_new;
+    }
+    if (lane != 0) return;
+    if (p.splits == 1) {
+        float* out = p.out + (static_cast<int64_t>(b) * p.L + l) * p.ldo + static_cast<int64_t>(h) * HD;
+#pragma unroll
+        for (int d = 0; d < HD; ++d) out[d] = total > 0.0f ? o[d] / total : 0.0f;
+    } else {
+        const int64_t slot = prow * p.splits + split;
+#pragma unroll
+        for (int d = 0; d < HD; ++d) p.partial_o[slot * HD + d] = o[d];
+        p.partial_ml[slot * 2] = m;
+        p.partial_ml[slot * 2 + 1] = total;
+    }
+}
+
+template <typename KT, int HD>
+int launch_small(const dlk_attention_params& p, hipStream_t stream) {
+    const int64_t rows = static_cast<int64_t>(p.B) * p.H * p.L;
+    hipLaunchKernelGGL((attention_small<KT, HD>), dim3(static_cast<unsigned>(rows), p.splits), dim3(kWave), 0, stream,
+                       p);
+    int status = static_cast<int>(hipGetLastError());
+    if (status != 0 || p.splits == 1 || p.partials_only) return status;
+    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, stream, p);
+    return static_cast<int>(hipGetLastError());
+}
+
 /// Whether the streaming decode kernel serves these heads (bf16 or f32 K/V, HD 64 or 128, G = 1, 2 or 4).
 bool stream_heads(int heads, int kv_heads, int hd, int kv_bf16) {
     (void)kv_bf16;
@@ -880,6 +954,14 @@ extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stre
         return p.hd == 64 ? dlk::launch_decode<float, 64>(p, stream) : static_cast<int>(hipErrorInvalidValue);
     }
     if (dlk_attention_prefill_eligible(&p)) return dlk_attention_prefill(&p, stream_handle);
+    if (p.hd < 16) {
+        switch (p.hd) {
+        case 2: return p.kv_bf16 ? dlk::launch_small<uint16_t, 2>(p, stream) : dlk::launch_small<float, 2>(p, stream);
+        case 4: return p.kv_bf16 ? dlk::launch_small<uint16_t, 4>(p, stream) : dlk::launch_small<float, 4>(p, stream);
+        case 8: return p.kv_bf16 ? dlk::launch_small<uint16_t, 8>(p, stream) : dlk::launch_small<float, 8>(p, stream);
+        default: return static_cast<int>(hipErrorInvalidValue);
+        }
+    }
     if (p.kv_bf16) {
         switch (p.hd) {
         case 16: return dlk::launch<uint16_t, 16>(p, stream);

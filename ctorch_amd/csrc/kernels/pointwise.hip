@@ -56,6 +56,12 @@ __global__ void copy_kernel(const void* src, int src_dtype, void* dst, int dst_d
             }
         } else if (src_dtype == DLK_I64 && dst_dtype == DLK_F64) {
             static_cast<double*>(dst)[d] = static_cast<double>(static_cast<const int64_t*>(src)[so]);
+        } else if (src_dtype == DLK_BF16 && dst_dtype == DLK_F32) {
+            // the bf16 codec on the bits (include/dl/half.h:60-66): a signalling NaN keeps its payload, which a
+            // round trip through double would quiet
+            static_cast<uint32_t*>(dst)[d] = static_cast<uint32_t>(static_cast<const uint16_t*>(src)[so]) << 16;
+        } else if (src_dtype == DLK_F32 && dst_dtype == DLK_BF16) {
+            static_cast<uint16_t*>(dst)[d] = f32_to_bf16(static_cast<const float*>(src)[so]);
         } else {
             store_from_double(dst, dst_dtype, d, load_as_double(src, src_dtype, so));
         }

@@ -208,8 +208,8 @@ Tensor grouped_query_attention(const Tensor& query, const Tensor& key, const Ten
     const Index KV = key.size(1), S = key.size(2);
     if (key.shape() != value.shape() || key.size(0) != B || key.size(3) != D || KV <= 0 || H % KV != 0)
         throw std::invalid_argument("grouped_query_attention: shapes differ or H is not a multiple of KV");
-    if (D != 16 && D != 32 && D != 64 && D != 128)
-        throw std::invalid_argument("grouped_query_attention: head size 16, 32, 64 or 128");
+    if (D != 2 && D != 4 && D != 8 && D != 16 && D != 32 && D != 64 && D != 128)
+        throw std::invalid_argument("grouped_query_attention: head size 2, 4, 8, 16, 32, 64 or 128");
     Tensor q = contiguous_f32(query.transpose(1, 2)); // [B, L, H, D] = rows (b, l)
     const DType kv_dtype = key.dtype() == DType::bf16 && value.dtype() == DType::bf16 ? DType::bf16 : DType::f32;
     Tensor k = key.dtype() == kv_dtype && key.is_contiguous() ? key : key.astype(kv_dtype).contiguous();

@@ -9,7 +9,9 @@
  * an output slot that is set to NULL on failure; status entries return DL_ERROR and keep the failure text
  * for the calling thread (dl_last_error); *_release accepts NULL.
  *
- * Device naming: dl_device_type value 1 is the HIP GPU (DL_GPU); the reference's DL_CUDA has the same value.
+ * Device naming: the reference's spellings are kept so that its C callers compile unchanged.  DL_CUDA (value 1)
+ * names the HIP GPU in this library, DL_GPU is an alias, and the pool statistics keep their dl_cuda_memory_*
+ * names (dl_gpu_memory_* are aliases).
  */
 #include "dl/export.h"
 
@@ -28,7 +30,7 @@ typedef struct dl_state dl_state;
 /* c_api.h:34-36,43,51,54-58,89 */
 typedef enum dl_status { DL_OK = 0, DL_ERROR = 1 } dl_status;
 typedef enum dl_dtype { DL_F32 = 0, DL_F64 = 1, DL_I64 = 2, DL_BOOL = 3, DL_F16 = 4, DL_BF16 = 5 } dl_dtype;
-typedef enum dl_device_type { DL_CPU = 0, DL_GPU = 1 } dl_device_type;
+typedef enum dl_device_type { DL_CPU = 0, DL_CUDA = 1, DL_GPU = DL_CUDA } dl_device_type;
 typedef struct dl_device { dl_device_type type; int32_t index; } dl_device;
 typedef struct dl_shape { const int64_t* data; size_t size; } dl_shape;
 typedef struct dl_tensor_options {
@@ -43,12 +45,13 @@ typedef struct dl_tensor_info {
     int32_t contiguous, requires_grad, leaf;
 } dl_tensor_info;
 typedef struct dl_random_key { uint64_t seed, stream; } dl_random_key;
-/* Pool statistics of this library's device allocator (reference dl_cuda_memory_stats, c_api.h:46-50). */
-typedef struct dl_gpu_memory_stats {
+/* Pool statistics of this library's device allocator (reference c_api.h:46-50). */
+typedef struct dl_cuda_memory_stats {
     uint64_t used_bytes, reserved_bytes;
     uint64_t peak_used_bytes, peak_reserved_bytes;
     uint64_t release_threshold;
-} dl_gpu_memory_stats;
+} dl_cuda_memory_stats;
+typedef dl_cuda_memory_stats dl_gpu_memory_stats;
 
 /* c_api.h:159-161 */
 DL_API const char* dl_version(void);
@@ -86,8 +89,14 @@ DL_API dl_status dl_embedding(const dl_tensor* indices, const dl_tensor* weight,
 DL_API dl_status dl_rms_norm(const dl_tensor* input, dl_shape normalized_shape,
     const dl_tensor* weight, const double* epsilon, dl_tensor** output);
 
-/* c_api.h:489-499: device synchronisation and allocator statistics (renamed from dl_cuda_memory_*) */
+/* c_api.h:488-499: grad mode, device synchronisation and the allocator's pool statistics */
 DL_API dl_status dl_synchronize(dl_device device);
+DL_API int32_t dl_grad_enabled(void);
+DL_API dl_status dl_cuda_memory_get_stats(int32_t device, dl_cuda_memory_stats* output);
+DL_API dl_status dl_cuda_memory_set_release_threshold(int32_t device, uint64_t bytes);
+DL_API dl_status dl_cuda_memory_reset_peak_stats(int32_t device);
+DL_API dl_status dl_cuda_memory_release_unused(int32_t device);
+/* the same four entries under this library's device name */
 DL_API dl_status dl_gpu_memory_get_stats(int32_t device, dl_gpu_memory_stats* output);
 DL_API dl_status dl_gpu_memory_set_release_threshold(int32_t device, uint64_t bytes);
 DL_API dl_status dl_gpu_memory_reset_peak_stats(int32_t device);

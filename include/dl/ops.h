@@ -13,8 +13,9 @@ DL_API Tensor argmax(const Tensor& input, Index axis, KeepDim keep = KeepDim::no
 /// Rotates interleaved pairs (2i, 2i+1) of the last axis by cosine/sine [L, D/2] (broadcast over leading
 /// axes, L = input.size(-2)).
 DL_API Tensor rotary_embedding(const Tensor& input, const Tensor& cosine, const Tensor& sine);
-/// Q [B,H,L,D], K [B,KV,S,D], V [B,KV,S,D]; query head h reads KV head h / (H/KV).  With no mask the
-/// causal rule of the decoder applies: query row l sees keys 0 .. S-L+l.
+/// Q [B,H,L,D], K [B,KV,S,D], V [B,KV,S,D]; query head h reads KV head h / (H/KV).  With no mask every query
+/// row sees all S keys, as in the reference (src/ops/attention.cpp:161-164: no causal window); the decoder's
+/// causal rule is applied by its own layers.  An explicit keep mask is not supported (throws).
 DL_API Tensor grouped_query_attention(const Tensor& query, const Tensor& key, const Tensor& value,
                                       std::optional<Tensor> keep_mask = std::nullopt);
 /// input [..., in] times weight [out, in]^T (+ bias [out]).

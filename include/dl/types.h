@@ -1,6 +1,8 @@
 #pragma once
-// Scalar types, devices and tensor options.  Mirrors include/dl/types.h:10-57 of the reference; the
-// accelerator is a HIP device named `gpu` (the C value 1 of dl_device_type is kept).
+// Scalar types, devices and tensor options.  Mirrors include/dl/types.h:10-57 of the reference.  The
+// accelerator keeps the reference's API spelling (DeviceType::cuda, Device::cuda(i), value 1) so that the
+// reference's callers compile unchanged; in this library it names HIP device i.  `gpu` is an alias of the
+// same value.
 
 #include "dl/export.h"
 #include "dl/half.h"
@@ -15,16 +17,17 @@ using Index = std::int64_t;
 using Shape = std::vector<Index>;
 
 enum class DType : std::uint8_t { f32, f64, i64, boolean, f16, bf16 };
-enum class DeviceType : std::uint8_t { cpu, gpu };
+enum class DeviceType : std::uint8_t { cpu, cuda, gpu = cuda };
 enum class KeepDim { no, yes };
 
-/// Where a storage lives.  The CPU device has index zero; `gpu(i)` is HIP device i.
+/// Where a storage lives.  The CPU device has index zero; `cuda(i)` (alias `gpu(i)`) is HIP device i.
 struct Device {
     DeviceType type = DeviceType::cpu;
     int index = 0;
 
     static constexpr Device cpu() { return {}; }
-    static constexpr Device gpu(int index = 0) { return {DeviceType::gpu, index}; }
+    static constexpr Device cuda(int index = 0) { return {DeviceType::cuda, index}; }
+    static constexpr Device gpu(int index = 0) { return cuda(index); }
     bool operator==(const Device&) const = default;
 };
 
