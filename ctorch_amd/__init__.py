@@ -129,6 +129,7 @@ SIGNATURES = {
     "dl_tensordot": (_st, [_p, _p, Shape, Shape, _pp]),
     "dl_rotary_embedding": (_st, [_p, _p, _p, _pp]),
     "dl_grouped_query_attention": (_st, [_p, _p, _p, _p, _pp]),
+    "dl_grouped_query_attention_noalloc": (_st, [_p, _p, _p, C.c_int, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i32]),
     "dl_swiglu_create": (_st, [_i64, _i64, _i32, TensorOptions, _pp]),
     "dl_lora_linear_create": (_st, [_p, _i64, _f64, _pp]),
     "dl_lora_linear_merge": (_st, [_p, _pp]),

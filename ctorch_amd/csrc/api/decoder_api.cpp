@@ -3,6 +3,8 @@
 #include "core/tensor_impl.h"
 #include "nn/decode_step.h"
 
+#include <cmath>
+
 #include <numeric>
 #include <stdexcept>
 
@@ -83,6 +85,52 @@ dl_status dl_grouped_query_attention(const dl_tensor* query, const dl_tensor* ke
         return dl::grouped_query_attention(require(query, "query").value, require(key, "key").value,
                                            require(value, "value").value,
                                            keep_mask ? std::optional<dl::Tensor>{keep_mask->value} : std::nullopt);
+    });
+}
+
+dl_status dl_grouped_query_attention_noalloc(const float* query, const void* key, const void* value, dl_dtype kv_dtype,
+                                             int64_t batch, int64_t heads, int64_t kv_heads, int64_t length,
+                                             int64_t source, int64_t head_dim, float* output, int32_t device) {
+    return invoke([&] {
+        if (!query || !key || !value || !output) throw std::invalid_argument("attention pointers must not be NULL");
+        if (kv_dtype != DL_F32 && kv_dtype != DL_BF16) throw std::invalid_argument("attention K/V dtype must be f32 or bf16");
+        if (batch <= 0 || heads <= 0 || kv_heads <= 0 || length <= 0 || heads % kv_heads != 0)
+            throw std::invalid_argument("attention dimensions must be positive and heads a multiple of kv_heads");
+        if (source < length) throw std::invalid_argument("attention needs source >= length");
+        const int64_t D = head_dim;
+        if (D != 2 && D != 4 && D != 8 && D != 16 && D != 32 && D != 64 && D != 128)
+            throw std::invalid_argument("attention head size 2, 4, 8, 16, 32, 64 or 128");
+        dlk_attention_params p{};
+        p.kv_bf16 = kv_dtype == DL_BF16;
+        dl::detail::attention_split(batch, heads, kv_heads, D, p.kv_bf16 != 0, length, source, p.splits, p.chunk);
+        const int64_t rows = batch * heads * length;
+        const int64_t need = p.splits > 1 ? rows * p.splits * (D + 2) : 0;
+        if (need > DLK_ATTENTION_SCRATCH_FLOATS)
+            throw std::invalid_argument("attention partials need " + std::to_string(need) +
+                                        " floats, more than the allocation-free entry's " +
+                                        std::to_string(DLK_ATTENTION_SCRATCH_FLOATS) + "-float scratch");
+        auto& context = dl::detail::gpu_context(device);
+        float* scratch = nullptr;
+        dl::detail::hip_check(dlk_attention_scratch(device, &scratch), "attention scratch");
+        p.q = query;
+        p.ldq = heads * D;
+        p.k = key;
+        p.v = value;
+        p.capacity = source;
+        p.first_host = source - length;
+        p.B = static_cast<int>(batch); p.L = static_cast<int>(length); p.H = static_cast<int>(heads);
+        p.KV = static_cast<int>(kv_heads); p.hd = static_cast<int>(D);
+        p.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
+        p.causal = 0;
+        p.out = output;
+        p.ldo = heads * D;
+        if (p.splits > 1) {
+            // every split writes its (max, sum) pair and, when it holds keys, its partial output row; the merge
+            // skips splits without keys, so nothing has to start at zero
+            p.partial_o = scratch;
+            p.partial_ml = scratch + rows * p.splits * D;
+        }
+        dl::detail::hip_check(dlk_attention(&p, context.stream), "grouped_query_attention_noalloc");
     });
 }
 

@@ -12,6 +12,7 @@
 #include "kernels/device_common.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace dlk {
@@ -927,6 +928,37 @@ int launch(const dlk_attention_params& p, hipStream_t stream) {
 
 } // namespace
 } // namespace dlk
+
+// Key-split partials of the allocation-free attention entry: a fixed array in device memory, one copy per GPU the
+// library runs on, held until the process ends.  Host code never passes the array's name to a kernel (on the host
+// it is only a stand-in for the symbol): dlk_attention_scratch resolves each device's own address once, with that
+// device current, and the launches take that address.
+static __device__ __align__(256) float scratch[DLK_ATTENTION_SCRATCH_FLOATS];
+
+extern "C" int dlk_attention_scratch(int device, float** address) {
+    constexpr int kDevicesMax = 64;
+    static std::mutex mutex;
+    static float* addresses[kDevicesMax] = {};
+    if (!address || device < 0 || device >= kDevicesMax) return static_cast<int>(hipErrorInvalidValue);
+    std::lock_guard<std::mutex> lock(mutex);
+    if (!addresses[device]) {
+        int current = 0;
+        hipError_t status = hipGetDevice(&current);
+        if (status != hipSuccess) return static_cast<int>(status);
+        if (current != device && (status = hipSetDevice(device)) != hipSuccess) return static_cast<int>(status);
+        void* found = nullptr;
+        status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+        if (current != device) {
+            const hipError_t restored = hipSetDevice(current);
+            if (status == hipSuccess) status = restored;
+        }
+        if (status != hipSuccess) return static_cast<int>(status);
+        if (!found) return static_cast<int>(hipErrorInvalidSymbol);
+        addresses[device] = static_cast<float*>(found);
+    }
+    *address = addresses[device];
+    return 0;
+}
 
 extern "C" int dlk_attention_decode_chunk(int heads, int kv_heads, int head_dim, int kv_bf16) {
     return dlk::decode_chunk_max(heads, kv_heads, head_dim, kv_bf16);

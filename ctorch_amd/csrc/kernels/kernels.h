@@ -145,6 +145,11 @@ int dlk_attention_stream_decode(int heads, int kv_heads, int head_dim, int kv_bf
 
 
 int dlk_attention(const dlk_attention_params* p, dlh_stream stream);
+/* Floats of the device-resident scratch array behind the allocation-free attention entry (8 MiB per GPU). */
+#define DLK_ATTENTION_SCRATCH_FLOATS (2 << 20)
+/* The address of that array on GPU `device` (looked up once per device with the device current; later calls
+   return the kept address). */
+int dlk_attention_scratch(int device, float** address);
 /* The matrix-core causal prefill kernel (attention_prefill.hip), which dlk_attention takes for causal launches
    over bf16 or f32 K/V, head dim 64 or 128, L >= 16 new positions, one split and H/KV dividing 128. */
 int dlk_attention_prefill_eligible(const dlk_attention_params* p);

@@ -22,6 +22,19 @@ DL_API dl_status dl_rotary_embedding(const dl_tensor* input, const dl_tensor* co
 DL_API dl_status dl_grouped_query_attention(const dl_tensor* query, const dl_tensor* key,
     const dl_tensor* value, const dl_tensor* keep_mask, dl_tensor** output);
 
+/* No counterpart in the reference: dl_grouped_query_attention for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops that forbid allocation).  The caller passes device pointers:
+ * query [B, L, H, D] f32 (position-major rows, head h at columns h*D), key and value [B, KV, S, D] contiguous in
+ * `kv_dtype` (DL_F32 or DL_BF16), output [B, L, H, D] f32.  The result is dl_grouped_query_attention's with no
+ * keep mask (every query row sees all S keys) and its kernels; key-split partials live in a fixed 8 MiB device
+ * array per GPU instead of allocated memory, and a shape whose partials would not fit (B*H*L * splits * (D + 2)
+ * floats) is rejected with DL_ERROR before anything runs.  Work is queued on the library's stream for `device`.
+ * The first call on a device sets up its context and the array's address; later calls allocate nothing.  Calls
+ * that overlap on one GPU share the array and race: issue them in order on that stream. */
+DL_API dl_status dl_grouped_query_attention_noalloc(const float* query, const void* key, const void* value,
+    dl_dtype kv_dtype, int64_t batch, int64_t heads, int64_t kv_heads, int64_t length, int64_t source,
+    int64_t head_dim, float* output, int32_t device);
+
 /* decoder_c_api.h:22-35 */
 DL_API dl_status dl_swiglu_create(int64_t dimensions, int64_t hidden, int32_t bias,
     dl_tensor_options options, dl_module** output);

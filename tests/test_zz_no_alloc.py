@@ -1,0 +1,71 @@
+"""The allocation-free attention entry (dl_grouped_query_attention_noalloc): through the C ABI, on device pointers
+the caller owns, against dl_grouped_query_attention on the same inputs, bit for bit (the same kernels and key
+splits; only the partials' home differs), on two calls in a row (the second smaller, reusing the scratch that
+the first left behind), with the device pool's used bytes unchanged by the calls, and with a shape whose partials
+exceed the scratch rejected before anything runs."""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import ctorch_amd as ct
+
+pytestmark = pytest.mark.gpu
+GPU = ct.device("gpu")
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def data(t):
+    return ct.lib().dl_tensor_data(t.handle)
+
+
+def reference_and_noalloc(rng, B, H, KV, L, S, D, kv_dtype):
+    q = rng.standard_normal((B, H, L, D)).astype(np.float32)
+    k = rng.standard_normal((B, KV, S, D)).astype(np.float32)
+    v = rng.standard_normal((B, KV, S, D)).astype(np.float32)
+    if kv_dtype == ct.BF16:  # bf16 bits of the same values (round to nearest even on the host)
+        k = (k.view(np.uint32) + 0x7FFF + ((k.view(np.uint32) >> 16) & 1) >> 16).astype(np.uint16)
+        v = (v.view(np.uint32) + 0x7FFF + ((v.view(np.uint32) >> 16) & 1) >> 16).astype(np.uint16)
+    gq, gk, gv = (ct.Tensor.from_numpy(q, None, GPU), ct.Tensor.from_numpy(k, kv_dtype, GPU),
+                  ct.Tensor.from_numpy(v, kv_dtype, GPU))
+    want = ct.grouped_query_attention(gq, gk, gv).numpy()          # [B, H, L, D]
+    q_rows = ct.Tensor.from_numpy(np.ascontiguousarray(q.transpose(0, 2, 1, 3)), None, GPU)  # [B, L, H, D]
+    out = ct.Tensor.from_numpy(np.full((B, L, H, D), np.nan, np.float32), None, GPU)
+    ct.synchronize()
+    before = ct.memory_stats().used_bytes
+    ct.check(ct.lib().dl_grouped_query_attention_noalloc(data(q_rows), data(gk), data(gv), kv_dtype, B, H, KV, L, S,
+                                                          D, data(out), 0))
+    ct.synchronize()
+    after = ct.memory_stats().used_bytes
+    got = out.numpy().transpose(0, 2, 1, 3)
+    return want, got, before, after
+
+
+def test_noalloc_attention_equals_the_allocating_entry_on_two_calls():
+    rng = np.random.default_rng(31)
+    # first call: 12 key splits on the streaming kernel (f32 K/V); sets up the device's scratch address
+    say("case: noalloc attention B=4 H=32 KV=8 L=1 S=3000 D=64 f32 (streaming kernel, 12 key splits)")
+    want, got, before, after = reference_and_noalloc(rng, 4, 32, 8, 1, 3000, 64, ct.F32)
+    assert np.array_equal(got, want)
+    # second call, smaller: 2 splits on the tile-per-wave kernel over bf16 K/V, on top of the first call's partials
+    say("case: noalloc attention B=2 H=32 KV=8 L=1 S=700 D=64 bf16 (decode kernel, 2 key splits)")
+    want, got, before, after = reference_and_noalloc(rng, 2, 32, 8, 1, 700, 64, ct.BF16)
+    assert np.array_equal(got, want)
+    assert after == before  # the call allocated nothing from the pool
+    say("case: noalloc attention several positions, head dim 128, f32")
+    want, got, before, after = reference_and_noalloc(rng, 2, 8, 2, 3, 300, 128, ct.F32)
+    assert np.array_equal(got, want) and after == before
+
+
+def test_noalloc_attention_rejects_partials_beyond_the_scratch():
+    # B*H*L * splits * (D + 2) floats above 2 Mi: refused before any pointer is read or any kernel runs
+    say("case: noalloc attention rejects B=32 H=32 KV=8 S=100000 D=128 (partials beyond the scratch)")
+    dummy = C.c_void_p(16)  # never dereferenced: the size check comes first
+    status = ct.lib().dl_grouped_query_attention_noalloc(dummy, dummy, dummy, ct.BF16, 32, 32, 8, 1, 100000, 128,
+                                                         dummy, 0)
+    assert status != 0 and "scratch" in ct.last_error()
