@@ -208,29 +208,104 @@ def decode_c1(ct, steps=128, prompt_len=32):
     return dict(ms=ms, steps=steps - 1)
 
 
-def cpu_baseline(prompt_len=4, decode_steps=8):
-    """The CPU oracle (plain-C restatement of the reference CPU path) on this host, one thread, at the C2 shape:
-    a short prompt is fed, then `decode_steps` single-token greedy steps are timed."""
+def host_cpu():
+    """The host's CPU model (from /proc/cpuinfo) and its logical CPU count."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 1
+
+
+def cpu_baseline(threads=16):
+    """The CPU oracle (plain-C restatement of the reference CPU path) on this host, per the plan of the reference's
+    CPU path: single-threaded as the reference's CPU kernels are, and, for the legs whose single-thread time would
+    run for minutes, a labelled row-parallel variant (bit-identical results) on `threads` threads.
+
+      C1  the tiny f32 decoder in full: 32-byte prompt, then 128 greedy steps (1 thread);
+      C2  1B bf16: the 128-token prompt (untimed setup, all threads), then 16 greedy decode steps timed (1 thread);
+      C3  1B bf16 at batch 32 over a 2048-token seeded prefix: 2 decode steps timed (`threads` threads);
+      C5  1B bf16 + LoRA r16: a 1 x 512 prefill sample timed (`threads` threads).
+    Weights are synthesised on the host with all threads before each leg (untimed)."""
     import oracle
     oracle.lib()
-    cfg = oracle.ModelConfig(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632,
-                             context=prompt_len + decode_steps + 1, dtype="bf16")
-    oracle.set_threads(min(16, os.cpu_count() or 1))
-    weights = oracle.synthesize_weights(cfg, (1234, 0))
-    lm = oracle.OracleLM(cfg, weights)
-    oracle.set_threads(1)
+    threads = max(1, min(threads, os.cpu_count() or 1))
+    model, nproc = host_cpu()
+    legs = {}
+
+    def lm_for(cfg, root):
+        oracle.set_threads(threads)
+        return oracle.OracleLM(cfg, oracle.synthesize_weights(cfg, root))
+
+    def timed(fn, n_threads):
+        oracle.set_threads(n_threads)
+        t0 = time.perf_counter()
+        out = fn()
+        return out, time.perf_counter() - t0
+
+    # C1
+    c1 = oracle.ModelConfig(vocab=256, layers=4, dimensions=256, heads=8, kv_heads=2, hidden=688, context=168,
+                            dtype="f32")
+    lm = lm_for(c1, (11, 0))
+    prompt = np.random.default_rng(11).integers(0, 256, size=(1, 32), dtype=np.int64)
+    _, sec = timed(lambda: lm.generate(prompt, 128), 1)
+    legs["c1"] = dict(value=128 / sec, unit="tok/s", cores=1, seconds=sec,
+                      sample="C1 in full: 32-byte prompt + 128 greedy steps (prompt included in the time)")
+    # C2
+    c2 = oracle.ModelConfig(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632, context=160,
+                            dtype="bf16")
+    lm = lm_for(c2, (1234, 0))
     cache = lm.make_cache(1)
-    ids = np.random.default_rng(7).integers(0, cfg.vocab, size=(1, prompt_len), dtype=np.int64)
-    logits = lm.logits(ids, cache)
-    token = logits[:, -1].argmax(-1).reshape(1, 1)
-    t0 = time.perf_counter()
-    for _ in range(decode_steps):
-        logits = lm.logits(token, cache)
-        token = logits[:, -1].argmax(-1).reshape(1, 1)
-    elapsed = time.perf_counter() - t0
-    return dict(value=decode_steps / elapsed, unit="tok/s", cores=1, kind="port",
-                sample=f"1B bf16 b=1 (C2 shape), {prompt_len}-token prompt then {decode_steps} greedy decode steps "
-                       f"timed ({elapsed:.1f} s), oracle/oracle.c -O3 -ffp-contract=off, 1 thread")
+    prompt = np.random.default_rng(7).integers(0, c2.vocab, size=(1, 128), dtype=np.int64)
+    oracle.set_threads(threads)
+    token = lm.logits(prompt, cache)[:, -1].argmax(-1).reshape(1, 1)
+
+    def c2_steps():
+        t = token
+        for _ in range(16):
+            t = lm.logits(t, cache)[:, -1].argmax(-1).reshape(1, 1)
+    _, sec = timed(c2_steps, 1)
+    legs["c2"] = dict(value=16 / sec, unit="tok/s", cores=1, seconds=sec,
+                      sample="C2: 128-token prompt (untimed), then 16 greedy decode steps at cache lengths 128-143")
+    # C3: the same 1B weights, batch 32 over a seeded 2048-token prefix (bf16-exact values, one block per layer)
+    B, P = 32, 2048
+    lm3 = oracle.OracleLM(oracle.ModelConfig(**{**c2.__dict__, "context": P + 4}), lm.w)
+    cache = lm3.make_cache(B)
+    n = B * c2.kv_heads * P * c2.head_dim
+    kv = [oracle.bf16_decode(oracle.bf16_encode(oracle.randn(oracle.fold_in((4242, 0), j), n)))
+          .reshape(B, c2.kv_heads, P, c2.head_dim) for j in (0, 1)]
+    for layer in range(c2.layers):
+        cache.fill(layer, P, kv[0], kv[1])
+    del kv
+    ids = np.random.default_rng(8).integers(0, c2.vocab, size=(B, 1), dtype=np.int64)
+
+    def c3_steps():
+        t = ids
+        for _ in range(2):
+            t = lm3.logits(t, cache)[:, -1].argmax(-1).reshape(B, 1)
+    _, sec = timed(c3_steps, threads)
+    legs["c3"] = dict(value=2 * B / sec, unit="tok/s", cores=threads, seconds=sec,
+                      sample="C3: batch 32 over a 2048-token seeded prefix, 2 greedy decode steps (row-parallel)")
+    del cache, lm3, lm
+    # C5
+    c5 = oracle.ModelConfig(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632, context=520,
+                            dtype="bf16", lora_rank=16, lora_alpha=32.0)
+    lm = lm_for(c5, (555, 0))
+    prompt = np.random.default_rng(10).integers(0, c5.vocab, size=(1, 512), dtype=np.int64)
+    cache = lm.make_cache(1)
+    _, sec = timed(lambda: lm.logits(prompt, cache), threads)
+    legs["c5"] = dict(value=512 / sec, unit="tok/s", cores=threads, seconds=sec,
+                      sample="C5: prefill of 1 x 512 tokens with unmerged LoRA r16 (row-parallel)")
+    c2leg = legs["c2"]
+    return dict(value=c2leg["value"], unit="tok/s", cores=1, kind="port",
+                sample=f"1B bf16 b=1 (C2): 128-token prompt then 16 greedy decode steps timed ({c2leg['seconds']:.1f} s), "
+                       f"oracle/oracle.c -O3 -ffp-contract=off, 1 thread",
+                cpu_model=model, nproc=nproc, legs=legs)
 
 
 def main():
@@ -319,9 +394,10 @@ def main():
 
     baseline = None
     if not args.no_cpu_baseline:
-        log("bench: CPU oracle baseline (single thread, bounded sample)")
+        log("bench: CPU oracle baseline (C1, C2 single thread; C3, C5 row-parallel samples)")
         baseline = cpu_baseline()
-        log(f"bench: CPU {baseline['value']:.3f} tok/s")
+        log("bench: CPU " + ", ".join(f"{k} {v['value']:.3g} {v['unit']} ({v['cores']} thr, {v['seconds']:.1f} s)"
+                                      for k, v in baseline["legs"].items()) + f" on {baseline['cpu_model']}")
 
     line = {
         "metric": "decode tok/s (1B bf16, b=1 and b=32) + achieved HBM GB/s vs MI355X peak",

@@ -284,8 +284,15 @@ std::vector<KernelTiming> DecoderLM::profile(const Tensor& ids, std::span<nn::KV
     const Device device = embedding_->weight().device();
     Tensor dev_ids = ids.to(device).contiguous();
     step_ = zeros({1}, {.dtype = DType::i64, .device = device});
-    next_ids_ = dev_ids.clone();
     tokens_ = Tensor();
+    // One unobserved step first: every workspace of the step reaches its size for this batch, so the buffers the
+    // recorded launches point at are the ones that stay (a later launch of the same step may otherwise grow and
+    // reallocate a workspace an earlier recorded launch uses).  The caches go back to their lengths afterwards.
+    const Index prefix = cache.front().length();
+    next_ids_ = dev_ids.clone();
+    forward_chunk(next_ids_.data<Index>(), B, 1, cache, 1, 0.0, {0, 0}, false, nullptr);
+    for (auto& c : cache) c.truncate(prefix);
+    next_ids_ = dev_ids.clone();
     ReplayObserver observer;
     forward_chunk(next_ids_.data<Index>(), B, 1, cache, 1, 0.0, {0, 0}, false, &observer);
     hip_check(dlh_stream_synchronize(context_->stream), "profile");

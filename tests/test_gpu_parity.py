@@ -367,6 +367,25 @@ def test_prefill_on_tiled_matrix_cores_with_lora_and_causal_attention(kv):
     assert rel_err(again, full) <= 1e-4
 
 
+def test_graph_decode_at_a_capacity_far_above_the_length_ignores_stale_workspace_memory():
+    # graph replay sizes the key splits for the cache capacity, so most splits hold no keys and never write their
+    # partial output rows; the merge must not read them.  The pool is first filled with NaN blocks and released, so
+    # the workspaces the decode allocates next are likely to reuse NaN-holding memory.
+    say("case: f32-cache decode at capacity 4096 over a 20-token prompt after NaN-filled pool blocks were released")
+    cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=512, context=4096,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(45, 0), scale=0.05)
+    stale = [G(np.full(n, np.nan, np.float32)) for n in (1 << 14, 1 << 16, 1 << 18, 1 << 20) for _ in range(8)]
+    ct.synchronize()
+    del stale
+    prompt = oracle.random_ids((46, 0), 20, cfg.vocab).reshape(1, 20)
+    tokens, last = gpu.generate(prompt, 12, use_graph=True)
+    assert np.all(np.isfinite(last))
+    history = np.concatenate([prompt, tokens[:, :-1]], 1)
+    teacher = ref.logits(history, ref.make_cache(1))[0, -1]
+    assert np.max(np.abs(last[0] - teacher)) <= 2e-2
+
+
 # ------------------------------------------------------------------------------------------ C2 shape
 def test_c2_1b_bf16_128_token_prompt_and_16_steps_against_the_f32_cache_oracle():
     say("case: C2 1B bf16 (16 layers, d=2048, 32/8 heads, F=5632, V=32000), 128-token prompt + 16 greedy steps, "
