@@ -550,10 +550,9 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-template <typename KT, int HD, int G, int TK>
-__global__ __launch_bounds__(4 * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_stream(
+template <typename KT, int HD, int G, int TK, int W>
+__global__ __launch_bounds__(W * kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_stream(
     const dlk_attention_params p) {
-    constexpr int W = 4;
     constexpr int ES = sizeof(KT);
     constexpr int DPL = 16 / ES;            // head-dim values per lane (one 16-byte piece)
     constexpr int LPK = HD * ES / 16;       // lanes per key row
@@ -830,14 +829,15 @@ bool stream_heads(int heads, int kv_heads, int hd, int kv_bf16) {
     return G == 1 || G == 2 || G == 4;
 }
 
-// Keys per tile: 32 bf16 / 16 f32 keys at HD 64, half that at HD 128 (the same 4 KB of K and of V per tile)
-template <typename KT, int HD, int TK = (HD == 64 ? 32 : 16) * 2 / static_cast<int>(sizeof(KT))>
+// bf16: four waves, tiles of 32 keys at HD 64 and 16 at HD 128 (4 KB of K and of V per tile).  f32: eight waves
+// (twice the bytes in flight per work-group), tiles of the same key counts (8 KB of K and of V per tile).
+template <typename KT, int HD, int TK = (HD == 64 ? 32 : 16), int W = sizeof(KT) == 4 ? 8 : 4>
 int launch_stream(const dlk_attention_params& p, hipStream_t stream) {
-    const dim3 grid(p.splits, p.B * p.KV), block(4 * kWave);
+    const dim3 grid(p.splits, p.B * p.KV), block(W * kWave);
     switch (p.H / p.KV) {
-    case 1: hipLaunchKernelGGL((attention_stream<KT, HD, 1, TK>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((attention_stream<KT, HD, 2, TK>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((attention_stream<KT, HD, 4, TK>), grid, block, 0, stream, p); break;
+    case 1: hipLaunchKernelGGL((attention_stream<KT, HD, 1, TK, W>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((attention_stream<KT, HD, 2, TK, W>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((attention_stream<KT, HD, 4, TK, W>), grid, block, 0, stream, p); break;
     default: return static_cast<int>(hipErrorInvalidValue);
     }
     int status = static_cast<int>(hipGetLastError());

@@ -84,12 +84,14 @@ void attention_split(Index batch, Index heads, Index kv_heads, Index head_dim, b
     constexpr Index tile = 64;
     if (length == 1 && dlk_attention_stream_decode(static_cast<int>(heads), static_cast<int>(kv_heads),
                                                    static_cast<int>(head_dim), kv_bf16 ? 1 : 0) &&
-        batch * kv_heads * source >= DLK_STREAM_DECODE_KEYS) {
-        // many keys: the streaming kernel, four waves per work-group each streaming its run of keys; runs of
-        // 64..256 keys sized for ~4096 waves in all (measured best at C3 and C4)
+        (batch * kv_heads * source >= DLK_STREAM_DECODE_KEYS || !kv_bf16)) {
+        // the streaming kernel: many keys in all, or any f32 cache.  Each wave streams its run of keys: runs of
+        // 64..256 keys sized for ~4096 runs in all (measured best at C3 and C4); four waves per work-group over a
+        // bf16 cache, eight over an f32 cache (whose rows are twice as long: a C2 step's 129-400 keys stay in one
+        // work-group per KV head, with twice the bytes in flight)
         const Index total = batch * kv_heads * source;
         const Index per_wave = std::clamp<Index>(((total + 4095) / 4096 + 63) / 64 * 64, 64, 256);
-        chunk = static_cast<int>(4 * per_wave);
+        chunk = static_cast<int>((kv_bf16 ? 4 : 8) * per_wave);
         splits = static_cast<int>((source + chunk - 1) / chunk);
         return;
     }
