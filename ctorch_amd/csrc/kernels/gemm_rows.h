@@ -22,7 +22,7 @@
 namespace dlk::gemm {
 
 using gemv::u32x4;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kTile = 16;                       // weight rows per wave tile
 constexpr int kMaxRows = 64;                    // activation rows per launch
@@ -103,9 +103,19 @@ __device__ __forceinline__ const uint16_t* tile_row(const TileMap& t, int i, int
     return t.base0 + static_cast<int64_t>(t.n0 + i) * K;
 }
 
-__device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
-    hi = f32_to_bf16(v);
-    lo = f32_to_bf16(v - bf16_to_f32(hi));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// bf16 hi and lo parts of four values (x = hi + lo to ~2^-16): the hardware's round-to-nearest-even conversion
+// packs two values per instruction, and the hi values are widened back from the packed words by shift and mask
+__device__ __forceinline__ void split4_bf16(const float (&e)[4], u32x2& hi, u32x2& lo) {
+    const f32x4v v = {e[0], e[1], e[2], e[3]};
+    const u32x2 h = __builtin_bit_cast(u32x2, __builtin_convertvector(v, bf16x4));
+    const f32x4v back = {__uint_as_float(h.x << 16), __uint_as_float(h.x & 0xffff0000u),
+                         __uint_as_float(h.y << 16), __uint_as_float(h.y & 0xffff0000u)};
+    hi = h;
+    lo = __builtin_bit_cast(u32x2, __builtin_convertvector(v - back, bf16x4));
 }
 
 // LoRA products of a lane's four tile rows, when the caller computed them (passed by value: a pointer to a
@@ -308,13 +318,10 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
             if (m >= p.M) v = make_float4(0.f, 0.f, 0.f, 0.f);
             squares[i] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             const float e[4] = {v.x * g[0], v.y * g[1], v.z * g[2], v.w * g[3]};
-            uint16_t h[4], l[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) split_bf16(e[j], h[j], l[j]);
-            *reinterpret_cast<uint2*>(hi + m * STRIDE + 4 * c4) =
-                make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
-            *reinterpret_cast<uint2*>(lo + m * STRIDE + 4 * c4) =
-                make_uint2(l[0] | (static_cast<uint32_t>(l[1]) << 16), l[2] | (static_cast<uint32_t>(l[3]) << 16));
+            u32x2 h, l;
+            split4_bf16(e, h, l);
+            *reinterpret_cast<u32x2*>(hi + m * STRIDE + 4 * c4) = h;
+            *reinterpret_cast<u32x2*>(lo + m * STRIDE + 4 * c4) = l;
         }
     };
     u32x4 wa[STEPS], wb[STEPS];

@@ -137,8 +137,8 @@ typedef struct dlk_attention_params {
 /* The widest decode chunk for this head layout (0 when the decode kernel does not apply). */
 int dlk_attention_decode_chunk(int heads, int kv_heads, int head_dim, int kv_bf16);
 /* One-position launches over at least this many keys in all (B * KV * splits * chunk) take the streaming decode
-   kernel when it serves the head layout: four waves per work-group, each streaming chunk / 4 keys (chunk a
-   multiple of 128). */
+   kernel when it serves the head layout: four waves per work-group over a bf16 cache and eight over an f32 cache,
+   each streaming chunk / waves keys (chunk a multiple of 64 * waves). */
 #define DLK_STREAM_DECODE_KEYS 32768
 /* 1 when the streaming decode kernel serves this head layout (bf16 or f32 K/V, head dim 64 or 128, H/KV <= 4). */
 int dlk_attention_stream_decode(int heads, int kv_heads, int head_dim, int kv_bf16);

@@ -85,13 +85,16 @@ void attention_split(Index batch, Index heads, Index kv_heads, Index head_dim, b
     if (length == 1 && dlk_attention_stream_decode(static_cast<int>(heads), static_cast<int>(kv_heads),
                                                    static_cast<int>(head_dim), kv_bf16 ? 1 : 0) &&
         (batch * kv_heads * source >= DLK_STREAM_DECODE_KEYS || !kv_bf16)) {
-        // the streaming kernel: many keys in all, or any f32 cache.  Each wave streams its run of keys: runs of
-        // 64..256 keys sized for ~4096 runs in all (measured best at C3 and C4); four waves per work-group over a
-        // bf16 cache, eight over an f32 cache (whose rows are twice as long: a C2 step's 129-400 keys stay in one
-        // work-group per KV head, with twice the bytes in flight)
+        // the streaming kernel: many keys in all, or any f32 cache.  Each wave streams its run of keys.  With
+        // 256 or more (sequence, KV head) pairs there is a work-group per pair already, so each takes all of its
+        // keys (no partials, no combine launch); below that, runs of 64..256 keys sized for ~4096 runs in all
+        // (measured best at C4).  Four waves per work-group over a bf16 cache, eight over an f32 cache (whose
+        // rows are twice as long: a C2 step's 129-400 keys stay in one work-group per KV head)
         const Index total = batch * kv_heads * source;
-        const Index per_wave = std::clamp<Index>(((total + 4095) / 4096 + 63) / 64 * 64, 64, 256);
-        chunk = static_cast<int>((kv_bf16 ? 4 : 8) * per_wave);
+        const Index waves = kv_bf16 ? 4 : 8;
+        Index per_wave = std::clamp<Index>(((total + 4095) / 4096 + 63) / 64 * 64, 64, 256);
+        if (batch * kv_heads >= 256) per_wave = ((source + waves - 1) / waves + 63) / 64 * 64;
+        chunk = static_cast<int>(waves * per_wave);
         splits = static_cast<int>((source + chunk - 1) / chunk);
         return;
     }

@@ -140,3 +140,16 @@ def test_constructor_and_cache_errors_follow_the_reference():
     with pytest.raises(ct.DLError, match="GPU only"):
         ct.decode(dec, x, cache)
     assert cache.length == 0
+
+
+def test_noalloc_attention_refuses_partials_beyond_its_scratch_before_any_device_call():
+    # B*H*L * splits * (D + 2) floats above 2 Mi: refused before any pointer is read or any HIP call is made, so
+    # this runs without a GPU.  128 (sequence, KV head) pairs over 100000 keys split the keys (98 splits of 1024):
+    # 512 rows * 98 * 130 floats.  (From 256 pairs up a work-group takes each pair whole and nothing is split.)
+    dummy = C.c_void_p(16)  # never dereferenced: the size check comes first
+    status = ct.lib().dl_grouped_query_attention_noalloc(dummy, dummy, dummy, ct.BF16, 16, 32, 8, 1, 100000, 128,
+                                                         dummy, 0)
+    assert status != 0 and "scratch" in ct.last_error(), ct.last_error()
+    # NULL pointers are refused whatever the shape
+    status = ct.lib().dl_grouped_query_attention_noalloc(None, dummy, dummy, ct.BF16, 1, 1, 1, 1, 1, 64, dummy, 0)
+    assert status != 0 and "NULL" in ct.last_error()
