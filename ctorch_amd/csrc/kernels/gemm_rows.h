@@ -9,8 +9,10 @@
 // 16).  The activation rows are staged per K-chunk in LDS as bf16 pairs hi + lo (x = hi + lo to ~2^-16), so every
 // product is two MFMAs and the result keeps f32-level accuracy against a bf16 weight.  The RMSNorm of the
 // activation rows is fused: the staged rows are x * g, the sums of squares accumulate while staging, and the
-// per-row factor 1/sqrt(mean x^2 + eps) scales the finished dot products.  Chunks are double buffered in LDS;
-// the next chunk's activations (into registers) and weights are loaded while the current chunk is used.
+// per-row factor 1/sqrt(mean x^2 + eps) scales the finished dot products.  A work-group of up to four chunks
+// (NC = 2 or 4) issues every activation and weight load of its chunks at once, stages them all, and computes: one
+// memory round trip.  Longer runs (NC = 0) double buffer the chunks in LDS, loading the next chunk's activations
+// (into registers) and weights while the current chunk is used.
 //
 // Tile rows: generic epilogues take 16 consecutive rows of one weight segment; SwiGLU interleaves gate and up
 // (tile row 2j = gate row 8T + j, 2j + 1 = up row 8T + j), so every lane holds (gate, up) pairs and QKV holds
@@ -32,7 +34,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 /// k per staged chunk: the double-buffered hi/lo rows stay within 64 KB of LDS.
 constexpr int chunk_k(int mt) { return mt == 1 ? 256 : mt == 2 ? 128 : 64; }
 constexpr int lds_stride(int mt) { return chunk_k(mt) + 8; } // bf16 elements per staged row (bank spread)
-constexpr size_t lds_bytes(int mt) { return size_t(2) * 2 * 16 * mt * lds_stride(mt) * 2; }
+/// LDS of a work-group: NC staged chunks (two for the double-buffered loop, NC = 0) of hi and lo rows.
+constexpr size_t lds_bytes(int mt, int nc) { return size_t(nc > 2 ? nc : 2) * 2 * 16 * mt * lds_stride(mt) * 2; }
+/// Up-front variant for a run of `nchunks` chunks: 2 or 4 (that many chunks at most), or 0 for the loop.
+constexpr int upfront_chunks(int nchunks) { return nchunks <= 2 ? 2 : nchunks <= 4 ? 4 : 0; }
+/// Most key slices a launch takes (the reduce kernel keeps them all in flight).
+constexpr int kMaxSplits = 16;
 
 /// Whether the matrix-core path takes these parameters (host side).
 inline bool eligible(const dlk_gemv_params& p) {
@@ -57,18 +64,19 @@ inline int blocks_of(const dlk_gemv_params& p) { return (tiles_of(p) + kWaves - 
 /// Activation tiles of 16 rows for a launch of `rows` (<= 64) rows.
 inline int row_tiles(int rows) { return rows <= 16 ? 1 : rows <= 32 ? 2 : 4; }
 
-/// Key slices of a launch: one, unless the weight tiles leave most CUs idle; then the fewest slices (each a
-/// whole number of chunks, at least two) that give 256 work-groups, or the most that divide the chunks.
+/// Key slices of a launch: one, unless the weight tiles leave most CUs idle; then the most slices (each a whole
+/// number of chunks; runs of one to four chunks take the up-front variant, longer ones the loop) that keep the
+/// launch within 256 work-groups, one per CU.  Measured on MI355X at batch 32 (1B widths):
+/// two work-groups on a CU, each with all of its loads in flight, stream slower than one (gate/up: 24.8 us at
+/// 352 work-groups, 21.0 at 176).
 inline int splits_of(const dlk_gemv_params& p, int rows) {
     if (p.epilogue == DLK_EPI_LOGITS) return 1;
     const int blocks = blocks_of(p);
     if (blocks >= 192) return 1;
     const int chunks = p.K / chunk_k(row_tiles(rows));
     int best = 1;
-    for (int s = 2; s <= 16; ++s) {
-        if (chunks % s != 0 || chunks / s < 2) continue;
-        best = s;
-        if (blocks * s >= 256) break;
+    for (int s = 2; s <= kMaxSplits && blocks * s <= 256; ++s) {
+        if (chunks % s == 0) best = s;
     }
     return best;
 }
@@ -245,7 +253,7 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
     }
 }
 
-template <int EPI, bool NORM, int MT>
+template <int EPI, bool NORM, int MT, int NC>
 __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
     constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
     constexpr int RM = 16 * MT;            // staged activation rows
@@ -283,9 +291,7 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
         const_cast<void*>(affine ? p.norm_weight : static_cast<const void*>(p.x)), 0, affine ? K * esize : 0,
         kBufferFlags);
 
-    float4 xr[XR];
-    u32x4 graw;
-    auto load_x = [&](int c) {
+    auto load_x = [&](int c, float4 (&xr)[XR], u32x4& graw) {
         const int k = k_begin + c * KC + 4 * c4;
 #pragma unroll
         for (int i = 0; i < XR; ++i) {
@@ -297,7 +303,7 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
     float squares[XR];
 #pragma unroll
     for (int i = 0; i < XR; ++i) squares[i] = 0.0f;
-    auto stage = [&](int buf) {
+    auto stage = [&](int buf, const float4 (&xr)[XR], const u32x4& graw) {
         float g[4] = {1.0f, 1.0f, 1.0f, 1.0f};
         if constexpr (NORM) {
             if (affine) {
@@ -350,41 +356,61 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
         }
     };
 
-    // Invariant at the top of each pair of chunks (c, c + 1): LDS buffer 0 holds chunk c, the registers hold
-    // chunk c + 1's activations, and the weights of c (wa) and c + 1 (wb) are loaded or in flight.  Loads in
-    // the loop are unconditional (a load on one path of a branch would drain every load at the next wait); the
-    // last two or three chunks are peeled.  nchunks >= 2 (the host requires K >= 2 * chunk).
-    load_x(0);
-    load_w(0, wa);
-    stage(0);
-    load_x(1);
-    load_w(1, wb);
-    gemv::lds_barrier();
-    int c = 0;
-    for (; c + 3 < nchunks; c += 2) {
-        compute(0, wa);
-        stage(1);
-        load_x(c + 2);
-        load_w(c + 2, wa);
+    if constexpr (NC > 0) {
+        // every load of the run first (chunks past the run repeat its last chunk: loads stay unconditional, so
+        // no branch drains them early), then the staging of the run's chunks into NC buffers and the products
+        float4 xs[NC][XR];
+        u32x4 gs[NC], ws[NC][STEPS];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) load_x(min(c, nchunks - 1), xs[c], gs[c]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) load_w(min(c, nchunks - 1), ws[c]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (c < nchunks) stage(c, xs[c], gs[c]);
         gemv::lds_barrier();
-        compute(1, wb);
-        stage(0);
-        load_x(c + 3);
-        load_w(c + 3, wb);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (c < nchunks) compute(c, ws[c]);
+    } else {
+        // Invariant at the top of each pair of chunks (c, c + 1): LDS buffer 0 holds chunk c, the registers hold
+        // chunk c + 1's activations, and the weights of c (wa) and c + 1 (wb) are loaded or in flight.  Loads in
+        // the loop are unconditional (a load on one path of a branch would drain every load at the next wait);
+        // the last two or three chunks are peeled.  nchunks >= 2 (the host requires K >= 2 * chunk).
+        float4 xr[XR];
+        u32x4 graw;
+        load_x(0, xr, graw);
+        load_w(0, wa);
+        stage(0, xr, graw);
+        load_x(1, xr, graw);
+        load_w(1, wb);
         gemv::lds_barrier();
-    }
-    compute(0, wa); // chunk c
-    stage(1);       // chunk c + 1
-    if (c + 2 < nchunks) {
-        load_x(c + 2);
-        load_w(c + 2, wa);
-    }
-    gemv::lds_barrier();
-    compute(1, wb); // chunk c + 1
-    if (c + 2 < nchunks) {
-        stage(0);
+        int c = 0;
+        for (; c + 3 < nchunks; c += 2) {
+            compute(0, wa);
+            stage(1, xr, graw);
+            load_x(c + 2, xr, graw);
+            load_w(c + 2, wa);
+            gemv::lds_barrier();
+            compute(1, wb);
+            stage(0, xr, graw);
+            load_x(c + 3, xr, graw);
+            load_w(c + 3, wb);
+            gemv::lds_barrier();
+        }
+        compute(0, wa);     // chunk c
+        stage(1, xr, graw); // chunk c + 1
+        if (c + 2 < nchunks) {
+            load_x(c + 2, xr, graw);
+            load_w(c + 2, wa);
+        }
         gemv::lds_barrier();
-        compute(0, wa); // chunk c + 2
+        compute(1, wb); // chunk c + 1
+        if (c + 2 < nchunks) {
+            stage(0, xr, graw);
+            gemv::lds_barrier();
+            compute(0, wa); // chunk c + 2
+        }
     }
 
     // per-row norm factor: every row belongs to one staging pass row, summed across the lanes that staged it
@@ -485,25 +511,47 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
     }
 }
 
+constexpr int kReduceThreads = 128;
+
 // Second launch of a key-split projection: thread (m, tile, q) sums the S partial dots of tile rows 4q .. 4q+3
-// for activation row m in slice order, applies the row's norm factor, and runs the lane epilogue.
+// for activation row m in slice order, applies the row's norm factor, and runs the lane epilogue.  All
+// kMaxSplits slices' loads are issued at once through buffer ranges that end at the launch's S slices: loads
+// past them read zero, and adding +0 after the S slices leaves every sum as the slice-order sum.
 template <int EPI, bool NORM>
-__global__ __launch_bounds__(kThreads) void gemm_reduce(const dlk_gemv_params p, int splits) {
+__global__ __launch_bounds__(kReduceThreads) void gemm_reduce(const dlk_gemv_params p, int splits) {
     constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
     const int tiles = tiles_of(p);
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kReduceThreads + threadIdx.x;
     const int q = static_cast<int>(idx % 4);
     const int tile = static_cast<int>((idx / 4) % tiles);
     const int m = static_cast<int>(idx / (4 * static_cast<int64_t>(tiles)));
     if (m < p.M) {
-        const int64_t width = static_cast<int64_t>(tiles) * kTile;
+        const int width = tiles * kTile;
+        const int plane = p.M * width; // floats per slice
+        const __amdgpu_buffer_rsrc_t dots = __builtin_amdgcn_make_buffer_rsrc(
+            p.split_partial, 0, splits * plane * static_cast<int>(sizeof(float)), kBufferFlags);
+        const __amdgpu_buffer_rsrc_t sums = __builtin_amdgcn_make_buffer_rsrc(
+            p.split_partial + static_cast<int64_t>(splits) * plane, 0, NORM ? splits * p.M * 4 : 0, kBufferFlags);
+        const int offset = (m * width + tile * kTile + 4 * q) * static_cast<int>(sizeof(float));
+        u32x4 part[kMaxSplits];
+        float row[kMaxSplits];
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s)
+            part[s] = __builtin_amdgcn_raw_buffer_load_b128(dots, offset + s * plane * 4, 0, 0);
+        if constexpr (NORM) {
+#pragma unroll
+            for (int s = 0; s < kMaxSplits; ++s)
+                row[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sums, (s * p.M + m) * 4, 0, 0));
+        }
         float v[4] = {0.f, 0.f, 0.f, 0.f};
         float squares = 0.0f;
-        for (int s = 0; s < splits; ++s) {
-            const float* part = p.split_partial + (static_cast<int64_t>(s) * p.M + m) * width + tile * kTile + 4 * q;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] += part[j];
-            if constexpr (NORM) squares += p.split_partial[static_cast<int64_t>(splits) * p.M * width + s * p.M + m];
+        for (int s = 0; s < kMaxSplits; ++s) {
+            v[0] += __uint_as_float(part[s].x);
+            v[1] += __uint_as_float(part[s].y);
+            v[2] += __uint_as_float(part[s].z);
+            v[3] += __uint_as_float(part[s].w);
+            if constexpr (NORM) squares += row[s];
         }
         const float inv = NORM && p.apply_norm ? rsqrtf(squares / static_cast<float>(p.K) + p.epsilon) : 1.0f;
 #pragma unroll
@@ -534,17 +582,25 @@ gemv::Kernel resolve_reduce(const dlk_gemv_params& p) {
     }
 }
 
-/// The matrix-core kernel for mt (1, 2 or 4) activation tiles; {} if none.
+/// The matrix-core kernel for mt (1, 2 or 4) activation tiles and nc (upfront_chunks) chunks; {} if none.
 template <int EPI>
-gemv::Kernel resolve(const dlk_gemv_params& p, int mt) {
+gemv::Kernel resolve(const dlk_gemv_params& p, int mt, int nc) {
     auto pick = [&](auto norm) -> gemv::Kernel {
         constexpr bool N = decltype(norm)::value;
-        switch (mt) {
-        case 1: return {reinterpret_cast<const void*>(&gemm_rows<EPI, N, 1>), lds_bytes(1)};
-        case 2: return {reinterpret_cast<const void*>(&gemm_rows<EPI, N, 2>), lds_bytes(2)};
-        case 4: return {reinterpret_cast<const void*>(&gemm_rows<EPI, N, 4>), lds_bytes(4)};
+#define DLK_GEMM_ROWS(MT, NC) {reinterpret_cast<const void*>(&gemm_rows<EPI, N, MT, NC>), lds_bytes(MT, NC)}
+        switch (mt * 8 + nc) {
+        case 8: return DLK_GEMM_ROWS(1, 0);
+        case 10: return DLK_GEMM_ROWS(1, 2);
+        case 12: return DLK_GEMM_ROWS(1, 4);
+        case 16: return DLK_GEMM_ROWS(2, 0);
+        case 18: return DLK_GEMM_ROWS(2, 2);
+        case 20: return DLK_GEMM_ROWS(2, 4);
+        case 32: return DLK_GEMM_ROWS(4, 0);
+        case 34: return DLK_GEMM_ROWS(4, 2);
+        case 36: return DLK_GEMM_ROWS(4, 4);
         default: return {};
         }
+#undef DLK_GEMM_ROWS
     };
     if (gemv::norm_variant(EPI, p.apply_norm != 0)) {
         if constexpr (EPI != DLK_EPI_RESIDUAL) return pick(std::true_type{});
@@ -556,11 +612,11 @@ gemv::Kernel resolve(const dlk_gemv_params& p, int mt) {
 
 } // namespace dlk::gemm
 
-dlk::gemv::Kernel dlk_gemm_kernel_store(const dlk_gemv_params& p, int mt);
-dlk::gemv::Kernel dlk_gemm_kernel_residual(const dlk_gemv_params& p, int mt);
-dlk::gemv::Kernel dlk_gemm_kernel_qkv(const dlk_gemv_params& p, int mt);
-dlk::gemv::Kernel dlk_gemm_kernel_swiglu(const dlk_gemv_params& p, int mt);
-dlk::gemv::Kernel dlk_gemm_kernel_logits(const dlk_gemv_params& p, int mt);
+dlk::gemv::Kernel dlk_gemm_kernel_store(const dlk_gemv_params& p, int mt, int nc);
+dlk::gemv::Kernel dlk_gemm_kernel_residual(const dlk_gemv_params& p, int mt, int nc);
+dlk::gemv::Kernel dlk_gemm_kernel_qkv(const dlk_gemv_params& p, int mt, int nc);
+dlk::gemv::Kernel dlk_gemm_kernel_swiglu(const dlk_gemv_params& p, int mt, int nc);
+dlk::gemv::Kernel dlk_gemm_kernel_logits(const dlk_gemv_params& p, int mt, int nc);
 dlk::gemv::Kernel dlk_gemm_reduce_store(const dlk_gemv_params& p);
 dlk::gemv::Kernel dlk_gemm_reduce_residual(const dlk_gemv_params& p);
 dlk::gemv::Kernel dlk_gemm_reduce_qkv(const dlk_gemv_params& p);

@@ -28,13 +28,13 @@ Kernel resolve(const dlk_gemv_params& p, int mt) {
 
 int activation_tile(int rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : 4; }
 
-Kernel resolve_gemm(const dlk_gemv_params& p, int mt) {
+Kernel resolve_gemm(const dlk_gemv_params& p, int mt, int nc) {
     switch (p.epilogue) {
-    case DLK_EPI_STORE: return dlk_gemm_kernel_store(p, mt);
-    case DLK_EPI_RESIDUAL: return dlk_gemm_kernel_residual(p, mt);
-    case DLK_EPI_QKV: return dlk_gemm_kernel_qkv(p, mt);
-    case DLK_EPI_SWIGLU: return dlk_gemm_kernel_swiglu(p, mt);
-    case DLK_EPI_LOGITS: return dlk_gemm_kernel_logits(p, mt);
+    case DLK_EPI_STORE: return dlk_gemm_kernel_store(p, mt, nc);
+    case DLK_EPI_RESIDUAL: return dlk_gemm_kernel_residual(p, mt, nc);
+    case DLK_EPI_QKV: return dlk_gemm_kernel_qkv(p, mt, nc);
+    case DLK_EPI_SWIGLU: return dlk_gemm_kernel_swiglu(p, mt, nc);
+    case DLK_EPI_LOGITS: return dlk_gemm_kernel_logits(p, mt, nc);
     default: return {};
     }
 }
@@ -99,11 +99,14 @@ int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
         if (params.epilogue != DLK_EPI_QKV) p.y = params.y ? params.y + static_cast<int64_t>(m0) * params.ldy : nullptr;
         if (params.residual) p.residual = params.residual + static_cast<int64_t>(m0) * params.ldres;
         p.bump_position = m0 + kMaxRows >= params.M ? params.bump_position : nullptr;
-        const Kernel kernel = resolve_gemm(p, row_tiles(p.M));
-        if (!kernel.fn) return static_cast<int>(hipErrorInvalidValue);
         // key slices when the tiles leave CUs idle and the caller gave room for the partials
         int splits = splits_of(p, p.M);
         if (splits > 1 && (!p.split_partial || p.split_capacity < split_floats(p, splits, p.M))) splits = 1;
+        // the reduce addresses the partials with 32-bit byte offsets
+        if (splits > 1 && split_floats(p, kMaxSplits, p.M) * 4 > INT32_MAX) splits = 1;
+        const int mt = row_tiles(p.M);
+        const Kernel kernel = resolve_gemm(p, mt, upfront_chunks(p.K / splits / chunk_k(mt)));
+        if (!kernel.fn) return static_cast<int>(hipErrorInvalidValue);
         const int64_t* bump = p.bump_position;
         if (splits > 1) p.bump_position = nullptr; // the reduce launch advances the length
         void* args[] = {&p};
@@ -115,8 +118,9 @@ int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
             if (!reduce.fn) return static_cast<int>(hipErrorInvalidValue);
             const int64_t threads = static_cast<int64_t>(p.M) * tiles_of(p) * 4;
             void* rargs[] = {&p, &splits};
-            status = hipLaunchKernel(reduce.fn, dim3(static_cast<unsigned>((threads + kThreads - 1) / kThreads)),
-                                     dim3(kThreads), rargs, 0, stream);
+            status = hipLaunchKernel(reduce.fn,
+                                     dim3(static_cast<unsigned>((threads + kReduceThreads - 1) / kReduceThreads)),
+                                     dim3(kReduceThreads), rargs, 0, stream);
             if (status != hipSuccess) return static_cast<int>(status);
         }
     }

@@ -5,8 +5,8 @@ dlk::gemv::Kernel dlk_gemv_kernel_qkv(const dlk_gemv_params& p, int mt) {
     return dlk::gemv::resolve<DLK_EPI_QKV>(p, mt);
 }
 
-dlk::gemv::Kernel dlk_gemm_kernel_qkv(const dlk_gemv_params& p, int mt) {
-    return dlk::gemm::resolve<DLK_EPI_QKV>(p, mt);
+dlk::gemv::Kernel dlk_gemm_kernel_qkv(const dlk_gemv_params& p, int mt, int nc) {
+    return dlk::gemm::resolve<DLK_EPI_QKV>(p, mt, nc);
 }
 
 dlk::gemv::Kernel dlk_gemm_reduce_qkv(const dlk_gemv_params& p) {

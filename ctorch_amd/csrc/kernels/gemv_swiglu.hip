@@ -5,8 +5,8 @@ dlk::gemv::Kernel dlk_gemv_kernel_swiglu(const dlk_gemv_params& p, int mt) {
     return dlk::gemv::resolve<DLK_EPI_SWIGLU>(p, mt);
 }
 
-dlk::gemv::Kernel dlk_gemm_kernel_swiglu(const dlk_gemv_params& p, int mt) {
-    return dlk::gemm::resolve<DLK_EPI_SWIGLU>(p, mt);
+dlk::gemv::Kernel dlk_gemm_kernel_swiglu(const dlk_gemv_params& p, int mt, int nc) {
+    return dlk::gemm::resolve<DLK_EPI_SWIGLU>(p, mt, nc);
 }
 
 dlk::gemv::Kernel dlk_gemm_reduce_swiglu(const dlk_gemv_params& p) {
