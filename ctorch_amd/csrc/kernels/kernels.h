@@ -132,16 +132,13 @@ typedef struct dlk_attention_params {
     int partials_only;       /* splits > 1: leave the merge of the partials to the caller (no combine launch) */
 } dlk_attention_params;
 
-/* Keys per split of the one-position decode kernel (L = 1): 256, 512 or 1024 (64 per wave; f32 K/V at most 512). */
-#define DLK_DECODE_CHUNK_MAX 1024
-/* The widest decode chunk for this head layout (0 when the decode kernel does not apply). */
-int dlk_attention_decode_chunk(int heads, int kv_heads, int head_dim, int kv_bf16);
-/* One-position launches over at least this many keys in all (B * KV * splits * chunk) take the streaming decode
-   kernel when it serves the head layout: four waves per work-group over a bf16 cache and eight over an f32 cache,
-   each streaming chunk / waves keys (chunk a multiple of 64 * waves). */
+/* Keys per split of a short one-position decode over a bf16 cache (few keys in all): 256 or 512, one work-group. */
+#define DLK_DECODE_CHUNK_MAX 512
+/* One-position decodes over at least this many keys in all (B * KV * keys), or over an f32 cache, split the keys
+   into runs of 64..256 keys per wave (~4096 runs in all; a work-group per (sequence, KV head) from 256 pairs). */
 #define DLK_STREAM_DECODE_KEYS 32768
-/* 1 when the streaming decode kernel serves this head layout (bf16 or f32 K/V, head dim 64 or 128, H/KV <= 4). */
-int dlk_attention_stream_decode(int heads, int kv_heads, int head_dim, int kv_bf16);
+/* 1 when the matrix-core one-position kernel serves this head layout (head dim 64 or 128, H/KV <= 16). */
+int dlk_attention_matrix_heads(int heads, int kv_heads, int head_dim);
 
 
 int dlk_attention(const dlk_attention_params* p, dlh_stream stream);
@@ -153,6 +150,10 @@ int dlk_attention_scratch(int device, float** address);
 /* The matrix-core causal prefill kernel (attention_prefill.hip), which dlk_attention takes for causal launches
    over bf16 or f32 K/V, head dim 64 or 128, L >= 16 new positions, one split and H/KV dividing 128. */
 int dlk_attention_prefill_eligible(const dlk_attention_params* p);
+/* One position on the matrix cores (attention_matrix.hip): eligibility, and the launch of the attention kernel
+   alone (with several splits it writes the partials; dlk_attention adds the merge). */
+int dlk_attention_matrix_eligible(const dlk_attention_params* p);
+int dlk_attention_matrix_decode(const dlk_attention_params* p, dlh_stream stream);
 int dlk_attention_prefill(const dlk_attention_params* p, dlh_stream stream);
 
 /* ------------------------------------------------------------------------------------------------------

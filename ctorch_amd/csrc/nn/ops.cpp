@@ -82,14 +82,14 @@ void linear_into(const float* x, Index rows, Index k, const Tensor& weight, cons
 void attention_split(Index batch, Index heads, Index kv_heads, Index head_dim, bool kv_bf16, Index length,
                      Index source, int& splits, int& chunk) {
     constexpr Index tile = 64;
-    if (length == 1 && dlk_attention_stream_decode(static_cast<int>(heads), static_cast<int>(kv_heads),
-                                                   static_cast<int>(head_dim), kv_bf16 ? 1 : 0) &&
-        (batch * kv_heads * source >= DLK_STREAM_DECODE_KEYS || !kv_bf16)) {
-        // the streaming kernel: many keys in all, or any f32 cache.  Each wave streams its run of keys.  With
+    const bool matrix = dlk_attention_matrix_heads(static_cast<int>(heads), static_cast<int>(kv_heads),
+                                                   static_cast<int>(head_dim)) != 0;
+    if (length == 1 && matrix && (batch * kv_heads * source >= DLK_STREAM_DECODE_KEYS || !kv_bf16)) {
+        // many keys in all, or an f32 cache: each wave of the matrix-core kernel streams its run of keys.  With
         // 256 or more (sequence, KV head) pairs there is a work-group per pair already, so each takes all of its
         // keys (no partials, no combine launch); below that, runs of 64..256 keys sized for ~4096 runs in all
-        // (measured best at C4).  Four waves per work-group over a bf16 cache, eight over an f32 cache (whose
-        // rows are twice as long: a C2 step's 129-400 keys stay in one work-group per KV head)
+        // (measured best at C4), counted as four waves per work-group over a bf16 cache and eight over an f32
+        // cache (whose rows are twice as long: a C2 step's 129-400 keys stay in one work-group per KV head)
         const Index total = batch * kv_heads * source;
         const Index waves = kv_bf16 ? 4 : 8;
         Index per_wave = std::clamp<Index>(((total + 4095) / 4096 + 63) / 64 * 64, 64, 256);
@@ -99,11 +99,10 @@ void attention_split(Index batch, Index heads, Index kv_heads, Index head_dim, b
         return;
     }
     if (length == 1) {
-        // one new position: one 64-key tile per wave, 4..16 waves per work-group merging in LDS; split only
-        // beyond the widest work-group (the split partials take a second, combine launch)
-        Index widest = dlk_attention_decode_chunk(static_cast<int>(heads), static_cast<int>(kv_heads),
-                                                  static_cast<int>(head_dim), kv_bf16 ? 1 : 0);
-        if (widest <= 0) widest = DLK_DECODE_CHUNK_MAX; // the general kernel takes any multiple of its tile
+        // one new position over few keys: one work-group of 256 or 512 keys (the matrix-core kernel; the general
+        // kernel for other head layouts takes up to 1024), split only beyond it (the split partials take a
+        // second, combine launch)
+        const Index widest = matrix ? DLK_DECODE_CHUNK_MAX : 16 * tile;
         Index per = 4 * tile;
         while (per < source && per < widest) per *= 2;
         chunk = static_cast<int>(per);

@@ -165,26 +165,32 @@ def test_operators_match_the_oracle():
         vv = rng.standard_normal((2, 2, S, 64)).astype(np.float32)
         y = ct.grouped_query_attention(G(qq), G(kk), G(vv)).numpy()
         assert np.max(np.abs(y - oracle.attention(qq, kk, vv, -1))) <= 1e-5
-    # one position over bf16 K/V: the decode kernel (4..16 waves of 64 keys per work-group); past the widest
-    # work-group the keys split and the combine launch merges the partials
+    # one position over few bf16 keys: the matrix-core kernel in one work-group of 256 or 512 keys; past it the
+    # keys split and the combine launch merges the partials (query heads per KV head: 4, 8, 16 and 1)
     for S, hd, heads in ((1, 64, 8), (64, 64, 8), (200, 64, 8), (257, 64, 8), (700, 64, 16), (300, 128, 8),
-                         (1500, 64, 8), (1100, 64, 2)):
+                         (1500, 64, 8), (1100, 64, 2), (300, 64, 32), (90, 128, 32)):
         qq = rng.standard_normal((2, heads, 1, hd)).astype(np.float32)
         kb = oracle.bf16_encode(rng.standard_normal((2, 2, S, hd)).astype(np.float32))
         vb = oracle.bf16_encode(rng.standard_normal((2, 2, S, hd)).astype(np.float32))
         y = ct.grouped_query_attention(G(qq), G(kb, ct.BF16), G(vb, ct.BF16)).numpy()
         want = oracle.attention(qq, oracle.bf16_decode(kb), oracle.bf16_decode(vb), -1)
         assert np.max(np.abs(y - want)) <= 2e-5, (S, hd, heads)
-        # the same keys and values held as f32: the f32 decode kernel (head dim 64), the streaming kernel (128)
+        # the same keys and values held as f32: the matrix-core kernel with the cache split into bf16 hi + lo
         yf = ct.grouped_query_attention(G(qq), G(oracle.bf16_decode(kb)), G(oracle.bf16_decode(vb))).numpy()
         assert np.max(np.abs(yf - want)) <= 2e-5, ("f32", S, hd, heads)
-    # many keys in all: the streaming kernel over f32 and bf16 K/V
-    for S, hd, heads in ((2100, 64, 8), (1500, 128, 8), (3000, 64, 2)):
-        qq = rng.standard_normal((8, heads, 1, hd)).astype(np.float32)
-        kk = rng.standard_normal((8, 2, S, hd)).astype(np.float32)
-        vv = rng.standard_normal((8, 2, S, hd)).astype(np.float32)
+    # many keys in all: key runs per wave over f32 and bf16 K/V; 256 (sequence, KV head) pairs take a work-group
+    # each (32 sequences x 8 KV heads)
+    for B, KV, S, hd, heads in ((8, 2, 2100, 64, 8), (8, 2, 1500, 128, 8), (8, 2, 3000, 64, 2), (32, 8, 200, 64, 32),
+                                (32, 8, 150, 128, 32)):
+        qq = rng.standard_normal((B, heads, 1, hd)).astype(np.float32)
+        kk = rng.standard_normal((B, KV, S, hd)).astype(np.float32)
+        vv = rng.standard_normal((B, KV, S, hd)).astype(np.float32)
         want = oracle.attention(qq, kk, vv, -1)
         assert np.max(np.abs(ct.grouped_query_attention(G(qq), G(kk), G(vv)).numpy() - want)) <= 2e-5, (S, hd)
+        kb, vb = oracle.bf16_encode(kk), oracle.bf16_encode(vv)
+        want = oracle.attention(qq, oracle.bf16_decode(kb), oracle.bf16_decode(vb), -1)
+        y = ct.grouped_query_attention(G(qq), G(kb, ct.BF16), G(vb, ct.BF16)).numpy()
+        assert np.max(np.abs(y - want)) <= 2e-5, ("bf16", B, S, hd)
     # several positions without a keep mask see every key (no causal window), over either K/V dtype
     for L, S, hd in ((20, 40, 64), (33, 33, 128)):
         qq = rng.standard_normal((2, 8, L, hd)).astype(np.float32)
@@ -297,8 +303,8 @@ def test_decode_over_split_keys_merges_partials(kv):
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
 @pytest.mark.parametrize("dimensions,heads,kv_heads", [(512, 8, 2), (512, 8, 4), (512, 8, 8), (1024, 8, 2)])
 def test_streaming_decode_attention_over_many_keys(dimensions, heads, kv_heads, kv):
-    # B * KV * prefix >= 32768 keys in all: one-position steps take the streaming decode kernel (4 waves per
-    # work-group, each streaming its run of keys, key splits merged by the combine launch)
+    # B * KV * prefix >= 32768 keys in all: one-position steps give each wave of the matrix-core kernel its own
+    # run of keys (key splits merged by the combine launch)
     B, P = 8, 2100
     say(f"case: streaming decode attention, d={dimensions} heads={heads}/{kv_heads}, B={B}, {P}-token {kv} prefix")
     cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=dimensions, heads=heads, kv_heads=kv_heads, hidden=512,
