@@ -201,11 +201,17 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const dlk_attention
 }
 
 // One work-group per (b, h, l) row merges its split partials: the global maximum first, then each thread takes
-// one head-dim column and every (256 / HD)-th split, and the column groups add up in LDS in a fixed order.
+// one head-dim column and every (512 / HD)-th split, and the column groups add up in LDS in a fixed order.  A
+// thread loads four of its splits at a time (the last group clamped to a valid split and discarded), so their
+// loads are in flight together; dead splits are dropped by selection, never by a branch around the loads.
+constexpr int kCombineThreads = 512;
+
 template <int HD>
-__global__ __launch_bounds__(kThreads) void attention_combine(const dlk_attention_params p) {
-    constexpr int GROUPS = kThreads / HD;
-    __shared__ float wave_max_s[kWaves];
+__global__ __launch_bounds__(kCombineThreads) void attention_combine(const dlk_attention_params p) {
+    constexpr int GROUPS = kCombineThreads / HD;
+    constexpr int WAVES = kCombineThreads / kWave;
+    constexpr int U = 4; // splits per thread in flight
+    __shared__ float wave_max_s[WAVES];
     __shared__ float acc_s[GROUPS][HD];
     __shared__ float total_s[GROUPS];
     const int64_t prow = blockIdx.x; // (b * H + h) * L + l
@@ -213,22 +219,33 @@ __global__ __launch_bounds__(kThreads) void attention_combine(const dlk_attentio
     const int64_t l = prow % p.L, h = (prow / p.L) % p.H, b = prow / (static_cast<int64_t>(p.L) * p.H);
     const float* ml = p.partial_ml + prow * p.splits * 2;
     float maximum = -INFINITY;
-    for (int s = t; s < p.splits; s += kThreads)
+    for (int s = t; s < p.splits; s += kCombineThreads)
         if (ml[2 * s + 1] > 0.0f) maximum = fmaxf(maximum, ml[2 * s]);
     maximum = wave_max(maximum);
     if (lane == 0) wave_max_s[t / kWave] = maximum;
     __syncthreads();
-    maximum = fmaxf(fmaxf(wave_max_s[0], wave_max_s[1]), fmaxf(wave_max_s[2], wave_max_s[3]));
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) maximum = fmaxf(maximum, wave_max_s[w]);
     const int d = t % HD, group = t / HD;
     float acc = 0.0f, total = 0.0f;
-    for (int s = group; s < p.splits; s += GROUPS) {
-        const float ms = ml[2 * s], ls = ml[2 * s + 1];
-        // a split without keys has weight 0 and an unwritten partial_o row: it must not enter the sum (0 * a
-        // stale NaN or Inf would)
-        if (!(ls > 0.0f && ms != -INFINITY)) continue;
-        const float w = expf(ms - maximum);
-        total += w * ls;
-        acc += w * p.partial_o[(prow * p.splits + s) * HD + d];
+    for (int s0 = group; s0 < p.splits; s0 += U * GROUPS) {
+        float ms[U], ls[U], o[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = min(s0 + u * GROUPS, p.splits - 1);
+            ms[u] = ml[2 * s];
+            ls[u] = ml[2 * s + 1];
+            o[u] = p.partial_o[(prow * p.splits + s) * HD + d];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            // a split without keys has weight 0 and an unwritten partial_o row: it must not enter the sum (0 * a
+            // stale NaN or Inf would), so it is selected away
+            const bool live = s0 + u * GROUPS < p.splits && ls[u] > 0.0f && ms[u] != -INFINITY;
+            const float w = live ? expf(ms[u] - maximum) : 0.0f;
+            total += live ? w * ls[u] : 0.0f;
+            acc += live ? w * o[u] : 0.0f;
+        }
     }
     acc_s[group][d] = acc;
     if (d == 0) total_s[group] = total;
@@ -315,14 +332,14 @@ int launch_small(const dlk_attention_params& p, hipStream_t stream) {
                        p);
     int status = static_cast<int>(hipGetLastError());
     if (status != 0 || p.splits == 1 || p.partials_only) return status;
-    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(rows)), dim3(kCombineThreads), 0, stream, p);
     return static_cast<int>(hipGetLastError());
 }
 
 template <int HD>
 int launch_combine(const dlk_attention_params& p, hipStream_t stream) {
     const int64_t combine_rows = static_cast<int64_t>(p.B) * p.H * p.L;
-    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kCombineThreads), 0, stream, p);
     return static_cast<int>(hipGetLastError());
 }
 
@@ -337,7 +354,7 @@ int launch(const dlk_attention_params& p, hipStream_t stream) {
     int status = static_cast<int>(hipGetLastError());
     if (status != 0 || p.splits == 1 || p.partials_only) return status;
     const int64_t combine_rows = static_cast<int64_t>(p.B) * p.H * p.L;
-    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((attention_combine<HD>), dim3(static_cast<unsigned>(combine_rows)), dim3(kCombineThreads), 0, stream, p);
     return static_cast<int>(hipGetLastError());
 }
 
