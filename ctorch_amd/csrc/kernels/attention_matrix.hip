@@ -21,7 +21,8 @@
 //
 // The products on the vector ALUs instead (eight lanes per key row, lane-group sums) cost ~600 vector instructions
 // per 32-key tile at G = 4, which bound a work-group per CU at ~4 TB/s (measured on MI355X: 32.9 us per layer at
-// batch 32 over 2048 bf16 keys, 25.7 us here); this kernel spends ~40 per tile.
+// batch 32 over 2048 bf16 keys, 25.7 us here); this kernel counts ~170 (the softmax, the V transpose, and the
+// wave's set-up and merge spread over its tiles) and 18 MFMAs per tile.
 #include "kernels/device_common.h"
 
 namespace dlk {
