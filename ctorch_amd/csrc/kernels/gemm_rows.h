@@ -160,7 +160,7 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
         const bool bias = EPI == DLK_EPI_STORE && p.bias;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int n = t.n0 + 4 * q + j;
+            const int n = (EPI == DLK_EPI_STORE ? gemv::seg_column(p, t.seg) : 0) + t.n0 + 4 * q + j;
             if constexpr (EPI == DLK_EPI_STORE) {
                 if (bias)
                     add[j] = p.bias_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.bias)[n])
@@ -171,7 +171,7 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int n = t.n0 + 4 * q + j;
+            const int n = (EPI == DLK_EPI_STORE ? gemv::seg_column(p, t.seg) : 0) + t.n0 + 4 * q + j;
             float out = v[j];
             if (EPI == DLK_EPI_RESIDUAL || bias) out += add[j];
             p.y[static_cast<int64_t>(m) * p.ldy + n] = out;
@@ -203,7 +203,7 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
                 odd += lora.v[2 * pair + 1] * p.lora_scale;
             } else if (hidden) {
                 // unmerged LoRA: + scale * up[n, :] . hidden[m, :]
-                const float* hrow = hidden + mg * p.lora_rank;
+                const float* hrow = hidden + mg * gemv::lora_stride(p);
                 float de = 0.0f, dodd = 0.0f;
                 for (int j = 0; j < p.lora_rank; ++j) {
                     de += Traits::scalar(lora_up, static_cast<int64_t>(n) * p.lora_rank + j) * hrow[j];
@@ -565,6 +565,141 @@ __global__ __launch_bounds__(kReduceThreads) void gemm_reduce(const dlk_gemv_par
     }
 }
 
+
+// Few weight tiles (a LoRA down projection: rank 16 per adapter) over several rows: one work-group per 16-row
+// tile, whose kWideWaves waves split K (K / kWideWaves keys each, every load of the wave issued at once) and merge
+// their dot products and row sums of squares in LDS in wave order; the first wave runs the lane epilogue.  One
+// launch and one memory round trip, where the key-split kernel would take a split launch and a reduce launch for
+// 2 tiles.  Each wave reads its activation fragments straight from memory (bf16 hi + lo in registers): the
+// re-read of the activation rows by every work-group is what makes this shape lose at many tiles.
+constexpr int kWideWaves = 16;
+constexpr int kWideTiles = 4;
+
+inline bool wide_eligible(const dlk_gemv_params& p) {
+    return p.epilogue != DLK_EPI_LOGITS && tiles_of(p) <= kWideTiles && p.M <= 32 && p.K % (32 * kWideWaves) == 0 &&
+           p.ldx % 4 == 0;
+}
+
+template <int EPI, bool NORM, int MT>
+__global__ __launch_bounds__(kWideWaves * kWave) void gemm_wide(const dlk_gemv_params p) {
+    constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
+    constexpr int RM = 16 * MT;
+    constexpr int D = MT == 1 ? 4 : 2; // k steps per batch of loads (within 128 registers at 16 waves)
+    __shared__ float red[kWideWaves][MT][4][kWave];
+    __shared__ float sq[kWideWaves][RM];
+    const int t = threadIdx.x, lane = t % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+    const int K = p.K, tile = blockIdx.x;
+    const int per = K / kWideWaves, steps = per / 32, kb = wave * per;
+    const TileMap tm = locate<SWIGLU>(p, tile);
+    const int i16 = lane % 16, g4 = lane / 16;
+    const uint16_t* wrow = tile_row<SWIGLU>(tm, i16, K) + kb + 8 * g4;
+    const bool norm = NORM && p.apply_norm;
+    const bool affine = norm && p.norm_weight;
+    const int esize = p.norm_bf16 ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t gres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(affine ? p.norm_weight : static_cast<const void*>(p.x)), 0, affine ? K * esize : 0,
+        kBufferFlags);
+    const float* xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        xrow[mt] = p.x + static_cast<int64_t>(min(16 * mt + i16, p.M - 1)) * p.ldx + kb + 8 * g4;
+    f32x4 acc[MT];
+    float squares[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        squares[mt] = 0.f;
+    }
+    for (int s0 = 0; s0 < steps; s0 += D) {
+        // the batch's loads first (steps past the wave's run repeat its last step and are not used)
+        u32x4 wv[D], gv[D][2];
+        float4 xv[D][MT][2];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int s = min(s0 + d, steps - 1);
+            wv[d] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + 32 * s));
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                xv[d][mt][0] = *reinterpret_cast<const float4*>(xrow[mt] + 32 * s);
+                xv[d][mt][1] = *reinterpret_cast<const float4*>(xrow[mt] + 32 * s + 4);
+            }
+            if constexpr (NORM) {
+                const int k = kb + 8 * g4 + 32 * s;
+                gv[d][0] = __builtin_amdgcn_raw_buffer_load_b128(gres, k * esize, 0, 0);
+                gv[d][1] = __builtin_amdgcn_raw_buffer_load_b128(gres, p.norm_bf16 ? gemv::kOutOfRange : (k + 4) * 4, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (s0 + d >= steps) break;
+            float g[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+            if constexpr (NORM) {
+                if (affine) {
+                    const u32x4 a = gv[d][0], c = gv[d][1];
+                    if (p.norm_bf16) {
+                        g[0] = bf16_lo(a.x); g[1] = bf16_hi(a.x); g[2] = bf16_lo(a.y); g[3] = bf16_hi(a.y);
+                        g[4] = bf16_lo(a.z); g[5] = bf16_hi(a.z); g[6] = bf16_lo(a.w); g[7] = bf16_hi(a.w);
+                    } else {
+                        g[0] = __uint_as_float(a.x); g[1] = __uint_as_float(a.y); g[2] = __uint_as_float(a.z);
+                        g[3] = __uint_as_float(a.w); g[4] = __uint_as_float(c.x); g[5] = __uint_as_float(c.y);
+                        g[6] = __uint_as_float(c.z); g[7] = __uint_as_float(c.w);
+                    }
+                }
+            }
+            const bf16x8 a = __builtin_bit_cast(bf16x8, wv[d]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                float4 v0 = xv[d][mt][0], v1 = xv[d][mt][1];
+                if (16 * mt + i16 >= p.M) v0 = v1 = make_float4(0.f, 0.f, 0.f, 0.f);
+                squares[mt] += v0.x * v0.x + v0.y * v0.y + v0.z * v0.z + v0.w * v0.w + v1.x * v1.x + v1.y * v1.y +
+                               v1.z * v1.z + v1.w * v1.w;
+                const float e0[4] = {v0.x * g[0], v0.y * g[1], v0.z * g[2], v0.w * g[3]};
+                const float e1[4] = {v1.x * g[4], v1.y * g[5], v1.z * g[6], v1.w * g[7]};
+                u32x2 h0, l0, h1, l1;
+                split4_bf16(e0, h0, l0);
+                split4_bf16(e1, h1, l1);
+                const u32x4 hh = {h0.x, h0.y, h1.x, h1.y}, ll = {l0.x, l0.y, l1.x, l1.y};
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, hh), acc[mt], 0, 0, 0);
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, ll), acc[mt], 0, 0, 0);
+            }
+        }
+    }
+    // merge the waves in wave order
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[wave][mt][j][lane] = acc[mt][j];
+        float s = squares[mt];
+        s += __shfl_xor(s, 16, kWave);
+        s += __shfl_xor(s, 32, kWave);
+        if (g4 == 0) sq[wave][16 * mt + i16] = s;
+    }
+    gemv::lds_barrier();
+    if (wave != 0) return;
+    double bs = 0.0;
+    int64_t bi = -1;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + i16;
+        float v[4] = {0.f, 0.f, 0.f, 0.f}, ss = 0.f;
+        for (int w = 0; w < kWideWaves; ++w) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] += red[w][mt][j][lane];
+            ss += sq[w][m];
+        }
+        if (m < p.M) {
+            const float inv = norm ? rsqrtf(ss / static_cast<float>(K) + p.epsilon) : 1.0f;
+            const float out[4] = {v[0] * inv * p.acc_scale, v[1] * inv * p.acc_scale, v[2] * inv * p.acc_scale,
+                                  v[3] * inv * p.acc_scale};
+            lane_epilogue<EPI>(p, tm, g4, m, out, bs, bi, p.key_seed, p.key_stream);
+        }
+    }
+    if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL) {
+        if (p.bump_position && blockIdx.x == 0 && t == 0) *p.bump_position += p.bump_count;
+    }
+}
+
 /// The reduce kernel of a key-split launch; {} if none.
 template <int EPI>
 gemv::Kernel resolve_reduce(const dlk_gemv_params& p) {
@@ -582,11 +717,19 @@ gemv::Kernel resolve_reduce(const dlk_gemv_params& p) {
     }
 }
 
-/// The matrix-core kernel for mt (1, 2 or 4) activation tiles and nc (upfront_chunks) chunks; {} if none.
+/// The matrix-core kernel for mt (1, 2 or 4) activation tiles and nc (upfront_chunks) chunks, or the few-tile
+/// kernel (nc = -1, mt 1 or 2); {} if none.
 template <int EPI>
 gemv::Kernel resolve(const dlk_gemv_params& p, int mt, int nc) {
     auto pick = [&](auto norm) -> gemv::Kernel {
         constexpr bool N = decltype(norm)::value;
+        if constexpr (EPI != DLK_EPI_LOGITS) {
+            if (nc < 0) {
+                if (mt == 1) return {reinterpret_cast<const void*>(&gemm_wide<EPI, N, 1>), 0};
+                if (mt == 2) return {reinterpret_cast<const void*>(&gemm_wide<EPI, N, 2>), 0};
+                return {};
+            }
+        }
 #define DLK_GEMM_ROWS(MT, NC) {reinterpret_cast<const void*>(&gemm_rows<EPI, N, MT, NC>), lds_bytes(MT, NC)}
         switch (mt * 8 + nc) {
         case 8: return DLK_GEMM_ROWS(1, 0);

@@ -390,7 +390,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
                     for (int h = 0; h < 2; ++h) {
                         const float* hidden = h == 0 ? p.lora_hidden[0] : p.lora_hidden[2];
                         if (!hidden) continue;
-                        const float* row = hidden + (p.m_base + min(m, p.M - 1)) * p.lora_rank + 8 * (lane_k ? q : 0);
+                        const float* row = hidden + (p.m_base + min(m, p.M - 1)) * gemv::lora_stride(p) + 8 * (lane_k ? q : 0);
                         const float4 a = *reinterpret_cast<const float4*>(row);
                         const float4 c = *reinterpret_cast<const float4*>(row + 4);
                         f32x8 x = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
@@ -428,7 +428,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
                 if constexpr (EPI == DLK_EPI_STORE || EPI == DLK_EPI_RESIDUAL) {
                     if (EPI == DLK_EPI_RESIDUAL || !p.bias) {
                         // four consecutive outputs of row m: one 16-byte store (and residual load)
-                        const int n = tm.n0 + 4 * q;
+                        const int n = (EPI == DLK_EPI_STORE ? gemv::seg_column(p, tm.seg) : 0) + tm.n0 + 4 * q;
                         float4 out = make_float4(v[0], v[1], v[2], v[3]);
                         if constexpr (EPI == DLK_EPI_RESIDUAL) {
                             const float4 r = *reinterpret_cast<const float4*>(p.residual + static_cast<int64_t>(m) * p.ldres + n);

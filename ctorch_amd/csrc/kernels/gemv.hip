@@ -99,6 +99,16 @@ int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
         if (params.epilogue != DLK_EPI_QKV) p.y = params.y ? params.y + static_cast<int64_t>(m0) * params.ldy : nullptr;
         if (params.residual) p.residual = params.residual + static_cast<int64_t>(m0) * params.ldres;
         p.bump_position = m0 + kMaxRows >= params.M ? params.bump_position : nullptr;
+        if (wide_eligible(p)) {
+            // few weight tiles: one launch, K split over the waves of each tile's work-group
+            const Kernel wide = resolve_gemm(p, row_tiles(p.M), -1);
+            if (!wide.fn) return static_cast<int>(hipErrorInvalidValue);
+            void* wargs[] = {&p};
+            const hipError_t status =
+                hipLaunchKernel(wide.fn, dim3(tiles_of(p)), dim3(kWideWaves * dlk::kWave), wargs, 0, stream);
+            if (status != hipSuccess) return static_cast<int>(status);
+            continue;
+        }
         // key slices when the tiles leave CUs idle and the caller gave room for the partials
         int splits = splits_of(p, p.M);
         if (splits > 1 && (!p.split_partial || p.split_capacity < split_floats(p, splits, p.M))) splits = 1;

@@ -232,6 +232,14 @@ __device__ __forceinline__ void load_aux(const dlk_gemv_params& p, const Group<W
     }
 }
 
+// First output column of segment seg in a STORE launch (the segments' outputs sit side by side in y).
+__device__ __forceinline__ int seg_column(const dlk_gemv_params& p, int seg) {
+    return seg == 0 ? 0 : seg == 1 ? p.seg_rows[0] : p.seg_rows[0] + p.seg_rows[1];
+}
+
+// Row stride of the LoRA hidden rows.
+__device__ __forceinline__ int64_t lora_stride(const dlk_gemv_params& p) { return p.lora_ld ? p.lora_ld : p.lora_rank; }
+
 // The epilogue of one finished group; v[m][r] holds the full dot products (every lane has them).
 template <typename WT, int MT, int R, int EPI, typename Seg>
 __device__ __forceinline__ void finish_group(const dlk_gemv_params& p, const Seg& sg, const float (&v)[MT][R], int g,
@@ -250,14 +258,16 @@ __device__ __forceinline__ void finish_group(const dlk_gemv_params& p, const Seg
                 const int n = n0 + r;
                 if (lane == m * R + r && m < p.M && n < seg_rows) {
                     float out = v[m][r];
+                    int col = n;
                     if constexpr (EPI == DLK_EPI_STORE) {
+                        col += seg_column(p, seg);
                         if (p.bias)
-                            out += p.bias_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.bias)[n])
-                                               : static_cast<const float*>(p.bias)[n];
+                            out += p.bias_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(p.bias)[col])
+                                               : static_cast<const float*>(p.bias)[col];
                     } else {
                         out += aux0;
                     }
-                    p.y[static_cast<int64_t>(m) * p.ldy + n] = out;
+                    p.y[static_cast<int64_t>(m) * p.ldy + col] = out;
                 }
             }
     } else if constexpr (SWIGLU) {
@@ -285,7 +295,7 @@ __device__ __forceinline__ void finish_group(const dlk_gemv_params& p, const Seg
                 if (hidden) {
                     // unmerged LoRA: + scale * up[n, :] . hidden[m, :] on both members of the pair
                     const int np = n ^ 1;
-                    const float* hrow = hidden + mg * p.lora_rank;
+                    const float* hrow = hidden + mg * lora_stride(p);
                     float dv = 0.0f, dp = 0.0f;
                     for (int j = 0; j < p.lora_rank; ++j) {
                         dv += Traits::scalar(lora_up, static_cast<int64_t>(n) * p.lora_rank + j) * hrow[j];

@@ -40,7 +40,7 @@ typedef struct dlk_gemv_params {
     const float* x;         /* [M, ldx] f32 */
     int64_t ldx;
     int M, K;
-    int nseg;               /* 1..3 weight segments stacked along n */
+    int nseg;               /* 1..3 weight segments stacked along n (STORE: their outputs side by side in y) */
     const void* w[3];       /* [seg_rows[i], K] row-major */
     int seg_rows[3];
     int w_bf16;
@@ -67,6 +67,7 @@ typedef struct dlk_gemv_params {
     int cache_bf16;
     int64_t cache_capacity;
     const float* lora_hidden[3]; /* per segment: [M_total, rank] f32 hidden = down(norm(x)) or NULL */
+    int64_t lora_ld;             /* row stride of the lora_hidden rows (0: lora_rank) */
     const void* lora_up[3];      /* per segment: [seg_rows, rank] */
     int lora_rank;
     float lora_scale;

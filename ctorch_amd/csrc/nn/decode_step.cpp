@@ -23,8 +23,7 @@ void DecodeWorkspace::ensure(const TransformerDecoderLayer& layer, Index n, Inde
         hidden = empty_tensor({n, d}, DType::f32, device);
         activation = empty_tensor({n, hidden_features}, DType::f32, device);
         splits_capacity = 0;
-        lora_query = Tensor();
-        lora_value = Tensor();
+        lora = Tensor();
     }
     const Index heads = layer.attention().heads();
     const Index partial_rows = n * heads; // one partial row per (b, h, l)
@@ -35,10 +34,9 @@ void DecodeWorkspace::ensure(const TransformerDecoderLayer& layer, Index n, Inde
     }
     const auto* qa = layer.attention().query_adapter();
     const auto* va = layer.attention().value_adapter();
-    if (qa && (!lora_query.defined() || lora_query.size(0) < n || lora_query.size(1) != qa->rank()))
-        lora_query = empty_tensor({n, qa->rank()}, DType::f32, device);
-    if (va && (!lora_value.defined() || lora_value.size(0) < n || lora_value.size(1) != va->rank()))
-        lora_value = empty_tensor({n, va->rank()}, DType::f32, device);
+    const Index ranks = (qa ? qa->rank() : 0) + (va ? va->rank() : 0);
+    if (ranks > 0 && (!lora.defined() || lora.size(0) < n || lora.size(1) != ranks))
+        lora = empty_tensor({n, ranks}, DType::f32, device);
 }
 
 void DecodeWorkspace::attach_workspace(dlk_gemv_params& p, Device device) {
@@ -91,28 +89,36 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         staged = tiled ? p.stage : nullptr;
     };
 
-    // 1. LoRA hidden states (down projections of the normalised input), when adapters are attached
-    auto lora_down = [&](const nn::LoRAAdapter* adapter, Tensor& hidden) {
-        if (!adapter) return;
-        int ab = 0, nb = 0;
+    // 1. LoRA hidden states (down projections of the normalised input), when adapters are attached: one launch
+    //    for both adapters, their down matrices as two weight segments whose outputs sit side by side in a row
+    //    of ws.lora (query adapter first)
+    const nn::LoRAAdapter* adapters[2] = {attention.query_adapter(), attention.value_adapter()};
+    const Index lora_width = ws.lora.defined() ? ws.lora.size(1) : 0;
+    if (adapters[0] || adapters[1]) {
+        int nb = 0, wb = -1;
         dlk_gemv_params p = gemv_params(x_in, rows, d, DLK_EPI_STORE);
         p.apply_norm = 1;
         p.norm_weight = norm_data(layer.attention_norm(), nb);
         p.norm_bf16 = nb;
         p.epsilon = static_cast<float>(layer.attention_norm().epsilon());
-        p.nseg = 1;
-        p.w[0] = weight_data(adapter->down().weight(), ab, "LoRA down");
-        p.seg_rows[0] = static_cast<int>(adapter->rank());
-        p.w_bf16 = ab;
-        p.y = static_cast<float*>(mutable_data(hidden));
-        p.ldy = adapter->rank();
+        double bytes = 0.0;
+        for (const auto* adapter : adapters) {
+            if (!adapter) continue;
+            int ab = 0;
+            p.w[p.nseg] = weight_data(adapter->down().weight(), ab, "LoRA down");
+            if (wb >= 0 && ab != wb) throw std::invalid_argument("LoRA adapters must share one dtype");
+            wb = ab;
+            p.seg_rows[p.nseg++] = static_cast<int>(adapter->rank());
+            bytes += static_cast<double>(adapter->down().weight().numel()) * (ab ? 2 : 4);
+        }
+        p.w_bf16 = wb;
+        p.y = static_cast<float*>(mutable_data(ws.lora));
+        p.ldy = lora_width;
         ws.attach_workspace(p, device);
         share_stage(p);
-        issue(observer, "lora_down", static_cast<double>(adapter->down().weight().numel()) * (ab ? 2 : 4),
+        issue(observer, "lora_down", bytes,
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "LoRA down projection"); });
-    };
-    lora_down(attention.query_adapter(), ws.lora_query);
-    lora_down(attention.value_adapter(), ws.lora_value);
+    }
 
     // 2. QKV projection: fused RMSNorm prologue, (LoRA,) RoPE and KV append epilogue
     {
@@ -144,18 +150,19 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         p.cache_capacity = cache.capacity();
         if (const auto* a = attention.query_adapter()) {
             int ub = 0;
-            p.lora_hidden[0] = ws.lora_query.data<float>();
+            p.lora_hidden[0] = ws.lora.data<float>();
             p.lora_up[0] = weight_data(a->up().weight(), ub, "LoRA up");
             p.lora_rank = static_cast<int>(a->rank());
             p.lora_scale = static_cast<float>(a->scale());
         }
         if (const auto* a = attention.value_adapter()) {
             int ub = 0;
-            p.lora_hidden[2] = ws.lora_value.data<float>();
+            p.lora_hidden[2] = ws.lora.data<float>() + (attention.query_adapter() ? attention.query_adapter()->rank() : 0);
             p.lora_up[2] = weight_data(a->up().weight(), ub, "LoRA up");
             p.lora_rank = static_cast<int>(a->rank());
             p.lora_scale = static_cast<float>(a->scale());
         }
+        p.lora_ld = lora_width;
         if (attention.query_adapter() && attention.value_adapter() &&
             (attention.query_adapter()->rank() != attention.value_adapter()->rank() ||
              attention.query_adapter()->scale() != attention.value_adapter()->scale()))

@@ -14,7 +14,8 @@ namespace dl::detail {
 /// Scratch of one decode chunk of `rows` = B * L activation rows.
 struct DecodeWorkspace {
     Index rows = 0, splits_capacity = 0;
-    Tensor q, attention, hidden, activation, partial_o, partial_ml, lora_query, lora_value;
+    Tensor q, attention, hidden, activation, partial_o, partial_ml;
+    Tensor lora; ///< LoRA hidden rows [rows, rank_q + rank_v]: the query adapter's, then the value adapter's
     Tensor split; ///< key-split partials of the matrix-core projections (shared: launches are stream-ordered)
     Tensor stage; ///< prefill projections: activation rows split into bf16 hi + lo, per-row norm factors
     /// Points `p` at the staging workspace when its shape takes the tiled prefill path and at the split
