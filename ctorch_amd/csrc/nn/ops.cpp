@@ -85,16 +85,22 @@ void attention_split(Index batch, Index heads, Index kv_heads, Index head_dim, b
     const bool matrix = dlk_attention_matrix_heads(static_cast<int>(heads), static_cast<int>(kv_heads),
                                                    static_cast<int>(head_dim)) != 0;
     if (length == 1 && matrix && (batch * kv_heads * source >= DLK_STREAM_DECODE_KEYS || !kv_bf16)) {
-        // many keys in all, or an f32 cache: each wave of the matrix-core kernel streams its run of keys.  With
-        // 256 or more (sequence, KV head) pairs there is a work-group per pair already, so each takes all of its
-        // keys (no partials, no combine launch); below that, runs of 64..256 keys sized for ~4096 runs in all
-        // (measured best at C4), counted as four waves per work-group over a bf16 cache and eight over an f32
-        // cache (whose rows are twice as long: a C2 step's 129-400 keys stay in one work-group per KV head)
+        // many keys in all, or an f32 cache: each wave of the matrix-core kernel streams its run of keys (four
+        // waves per work-group when the keys split).  With 256 or more (sequence, KV head) pairs there is a
+        // work-group per pair already, so each takes all of its keys (no partials, no combine launch: C3); an
+        // f32 cache of at most 512 keys stays in one work-group per pair (C2: eight waves); otherwise runs of
+        // 64..256 keys per wave, about total / 1024 keys over a bf16 cache and total / 512 over an f32 cache
+        // (measured on MI355X at b=4 over 4100 keys: bf16 14.6 us per layer at 192 keys per wave against 15.8 at
+        // 64 and 256; f32 23.8 us at 256 against 26.5 at 128; C4 keeps 256)
         const Index total = batch * kv_heads * source;
-        const Index waves = kv_bf16 ? 4 : 8;
-        Index per_wave = std::clamp<Index>(((total + 4095) / 4096 + 63) / 64 * 64, 64, 256);
-        if (batch * kv_heads >= 256) per_wave = ((source + waves - 1) / waves + 63) / 64 * 64;
-        chunk = static_cast<int>(waves * per_wave);
+        if (batch * kv_heads >= 256) {
+            chunk = static_cast<int>(4 * (((source + 3) / 4 + 63) / 64 * 64));
+        } else if (!kv_bf16 && source <= DLK_DECODE_CHUNK_MAX) {
+            chunk = DLK_DECODE_CHUNK_MAX;
+        } else {
+            const Index per_run = kv_bf16 ? 1024 : 512;
+            chunk = static_cast<int>(4 * std::clamp<Index>(((total + per_run - 1) / per_run + 63) / 64 * 64, 64, 256));
+        }
         splits = static_cast<int>((source + chunk - 1) / chunk);
         return;
     }

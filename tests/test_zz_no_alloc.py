@@ -47,8 +47,8 @@ def reference_and_noalloc(rng, B, H, KV, L, S, D, kv_dtype):
 
 def test_noalloc_attention_equals_the_allocating_entry_on_two_calls():
     rng = np.random.default_rng(31)
-    # first call: 6 key splits of 512 keys (f32 K/V); sets up the device's scratch address
-    say("case: noalloc attention B=4 H=32 KV=8 L=1 S=3000 D=64 f32 (matrix-core kernel, 6 key splits)")
+    # first call: 4 key splits of 768 keys (f32 K/V); sets up the device's scratch address
+    say("case: noalloc attention B=4 H=32 KV=8 L=1 S=3000 D=64 f32 (matrix-core kernel, 4 key splits)")
     want, got, before, after = reference_and_noalloc(rng, 4, 32, 8, 1, 3000, 64, ct.F32)
     assert np.array_equal(got, want)
     # second call, smaller: 2 splits over bf16 K/V, on top of the first call's partials
