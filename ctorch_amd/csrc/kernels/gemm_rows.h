@@ -133,6 +133,46 @@ struct LoraProducts {
     bool set;
 };
 
+// Unmerged LoRA of the output pair (n, n + 1): up[n, :] . h and up[n + 1, :] . h over the rank, for a bf16 up
+// matrix.  Ranks of 8..32 in steps of 8 issue every load first (16-byte pieces of both up rows and of h; pieces
+// past the rank repeat the last one and are not used), so the pair costs one memory round trip instead of one per
+// rank entry; other ranks take the scalar loop.
+constexpr int kLoraPiecesMax = 4; // rank 32
+__device__ __forceinline__ void lora_pair(const dlk_gemv_params& p, const void* up, const float* hrow, int n,
+                                          float& de, float& dodd) {
+    using Traits = gemv::WeightTraits<uint16_t>;
+    const int r = p.lora_rank;
+    de = 0.0f;
+    dodd = 0.0f;
+    if (r % 8 == 0 && r <= 8 * kLoraPiecesMax && gemv::lora_stride(p) % 4 == 0) {
+        const int pieces = r / 8;
+        const uint16_t* ue = static_cast<const uint16_t*>(up) + static_cast<int64_t>(n) * r;
+        u32x4 we[kLoraPiecesMax], wo[kLoraPiecesMax];
+        float h[kLoraPiecesMax][8];
+#pragma unroll
+        for (int s = 0; s < kLoraPiecesMax; ++s) {
+            const int k = 8 * min(s, pieces - 1);
+            we[s] = *reinterpret_cast<const u32x4*>(ue + k);
+            wo[s] = *reinterpret_cast<const u32x4*>(ue + r + k);
+            const float4 a = *reinterpret_cast<const float4*>(hrow + k);
+            const float4 c = *reinterpret_cast<const float4*>(hrow + k + 4);
+            h[s][0] = a.x; h[s][1] = a.y; h[s][2] = a.z; h[s][3] = a.w;
+            h[s][4] = c.x; h[s][5] = c.y; h[s][6] = c.z; h[s][7] = c.w;
+        }
+#pragma unroll
+        for (int s = 0; s < kLoraPiecesMax; ++s) {
+            if (s >= pieces) break;
+            de += Traits::dot(we[s], h[s]);
+            dodd += Traits::dot(wo[s], h[s]);
+        }
+        return;
+    }
+    for (int j = 0; j < r; ++j) {
+        de += Traits::scalar(up, static_cast<int64_t>(n) * r + j) * hrow[j];
+        dodd += Traits::scalar(up, static_cast<int64_t>(n + 1) * r + j) * hrow[j];
+    }
+}
+
 // QKV: the batch and cache position of activation row m, when the caller computed them once for the row
 // (they take a 64-bit division).
 struct RowPosition {
@@ -148,7 +188,6 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
                                               const float (&v)[4], double& best_score, int64_t& best_index,
                                               uint64_t seed, uint64_t stream, LoraProducts lora = {{}, false},
                                               RowPosition where = {0, 0, false}) {
-    using Traits = gemv::WeightTraits<uint16_t>;
     if constexpr (EPI == DLK_EPI_SWIGLU) {
         const int n = t.n0 + 2 * q;
         p.y[static_cast<int64_t>(m) * p.ldy + n] = gemv::silu(v[0]) * v[1];
@@ -203,12 +242,8 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
                 odd += lora.v[2 * pair + 1] * p.lora_scale;
             } else if (hidden) {
                 // unmerged LoRA: + scale * up[n, :] . hidden[m, :]
-                const float* hrow = hidden + mg * gemv::lora_stride(p);
-                float de = 0.0f, dodd = 0.0f;
-                for (int j = 0; j < p.lora_rank; ++j) {
-                    de += Traits::scalar(lora_up, static_cast<int64_t>(n) * p.lora_rank + j) * hrow[j];
-                    dodd += Traits::scalar(lora_up, static_cast<int64_t>(n + 1) * p.lora_rank + j) * hrow[j];
-                }
+                float de, dodd;
+                lora_pair(p, lora_up, hidden + mg * gemv::lora_stride(p), n, de, dodd);
                 even += de * p.lora_scale;
                 odd += dodd * p.lora_scale;
             }
