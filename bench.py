@@ -9,7 +9,8 @@ the GPU: embedding gather -> 16 fused layers -> final norm + LM head -> sampling
 HIP graph; exactly --steps steps are timed with HIP events on the library's compute stream after --warmup
 untimed steps.
 
-Also reported: the b=32 decode over a 2048-token seeded K/V prefix (configs[2], "C3"), the 8B-class b=8 decode over
+Also reported: the same C2 decode with temperature-1.0 sampling under an explicit key (configs[1]'s second leg),
+the b=32 decode over a 2048-token seeded K/V prefix (configs[2], "C3"), the 8B-class b=8 decode over
 a 32768-token seeded K/V prefix (configs[3], "C4"), the per-kernel roofline of
 the dominant kernel (gate/up projection: each layer's launch repeated back to back between two HIP events on the
 compute stream), a streaming-copy bandwidth reference, and the CPU oracle timed on this host (single thread) on
@@ -108,12 +109,19 @@ def kv_bytes(cfg, batch, length, element=4):
     return element * batch * cfg["layers"] * 2 * cfg["kv_heads"] * hd * length
 
 
+SAMPLE_KEY = (2024, 7)  # the explicit random key of the sampled C2 leg
+
+
 def decode_b1(ct, steps, warmup):
     context = 128 + 3 + warmup + steps + 8
     decoder, lm = build_model(ct, C2, max(384, context))
     prompt = np.random.default_rng(7).integers(0, C2["vocab"], size=(1, 128), dtype=np.int64)
     cache = ct.DecoderCache(decoder)
     ms, tokens = lm.benchmark(prompt, cache, warmup, steps, 0.0, (0, 0), True)
+    # the same decode with temperature-1.0 explicit-key sampling (BASELINE's second C2 leg), on a fresh cache
+    scache = ct.DecoderCache(decoder)
+    sampled_ms, _ = lm.benchmark(prompt, scache, warmup, steps, 1.0, SAMPLE_KEY, True)
+    del scache
     # mean cache length over the timed steps: prompt + tokens before them, + the step's own key
     first = 128 + 3 + warmup
     mean_len = first + (steps - 1) / 2.0
@@ -123,7 +131,8 @@ def decode_b1(ct, steps, warmup):
     pcache = ct.DecoderCache(decoder)
     lm.logits(prompt, pcache)
     timings = lm.profile(prompt[:, -1:], pcache, 10)
-    return dict(ms=ms, step_bytes=step_bytes, timings=timings, tokens=tokens, mean_len=mean_len), decoder, lm
+    return dict(ms=ms, sampled_ms=sampled_ms, step_bytes=step_bytes, timings=timings, tokens=tokens,
+                mean_len=mean_len), decoder, lm
 
 
 def decode_b32(ct, steps, warmup, prefix=2048):
@@ -336,6 +345,8 @@ def main():
     tok_s = args.steps / (b1["ms"] / 1e3)
     achieved = b1["step_bytes"] / (ms_per_step / 1e3) / 1e9
     log(f"bench: b=1 {ms_per_step * 1e3:.1f} us/step, {tok_s:.0f} tok/s, {achieved:.0f} GB/s algorithmic")
+    sampled_us = 1e3 * b1["sampled_ms"] / args.steps
+    log(f"bench: b=1 temperature 1.0 (explicit key) {sampled_us:.1f} us/step, {1e6 / sampled_us:.0f} tok/s")
 
     gate = next(t for t in b1["timings"] if t["name"] == "gate_up_silu")
     gate_avg_ms = gate["total_ms"] / gate["launches"]
@@ -345,7 +356,8 @@ def main():
                            "GB/s": (t["bytes"] / t["total_ms"] * 1e-6) if t["total_ms"] > 0 and t["bytes"] else None}
                for t in b1["timings"]}
 
-    extra = {}
+    extra = {"c2_sampled": {"tok_s": 1e6 / sampled_us, "us_per_step": sampled_us, "temperature": 1.0,
+                            "key": list(SAMPLE_KEY), "steps": args.steps, "warmup": args.warmup}}
     c1 = decode_c1(ct)
     extra["c1"] = {"tok_s": c1["steps"] / (c1["ms"] / 1e3), "us_per_step": 1e3 * c1["ms"] / c1["steps"],
                    "steps": c1["steps"], "prompt": 32, "dtype": "f32"}
