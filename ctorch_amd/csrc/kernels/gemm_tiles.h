@@ -30,6 +30,7 @@
 
 namespace dlk::tiles {
 
+using gemm::bf16x4;
 using gemm::bf16x8;
 using gemm::f32x4;
 using gemv::u32x4;
@@ -348,7 +349,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
 
     const int q = lane / 16;
     if constexpr (SWIGLU) {
-        // lane holds gate (slot i) and up (slot i + 4) of features 128 n_blk + 16 (4 wn + i) + 4 q .. +4
+        // lane holds gate (slot i) and up (slot i + 4) of features 128 n_blk + 16 (4 wn + i) + 4 q .. +4.  With
+        // stage_out the four products go to the next launch's staging layout (feature f = its k): hi and lo of
+        // row m, k step f / 32, lane (m % 16) + 16 ((f % 32) / 8), elements f % 8 .. +4, the split that
+        // prepare_rows would make of the f32 rows.  Rows from M up to the 256-row block hold the products of the
+        // staged rows past M (copies of row M - 1), as prepare_rows writes them.
+        const int out_steps = p.seg_rows[0] / 32;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int f = 128 * n_blk + 16 * (4 * wn + i) + 4 * q;
@@ -356,12 +362,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int m = m_first + 64 * wm + 16 * j + lane % 16;
-                if (m >= p.M) continue;
+                if (m >= p.M && !p.stage_out) continue;
                 const float scale = inv[j] * p.acc_scale;
                 float o[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) o[r] = gemv::silu(acc[i][j][r] * scale) * (acc[i + 4][j][r] * scale);
-                *reinterpret_cast<float4*>(p.y + static_cast<int64_t>(m) * p.ldy + f) = make_float4(o[0], o[1], o[2], o[3]);
+                if (p.stage_out) {
+                    const f32x4 v = {o[0], o[1], o[2], o[3]};
+                    const bf16x4 h = __builtin_convertvector(v, bf16x4);
+                    const bf16x4 l = __builtin_convertvector(v - __builtin_convertvector(h, f32x4), bf16x4);
+                    char* at = static_cast<char*>(p.stage_out) +
+                               (static_cast<int64_t>(m / 16) * out_steps + f / 32) * 2048 +
+                               ((m % 16) + 16 * ((f % 32) / 8)) * 16 + (f % 8) * 2;
+                    *reinterpret_cast<bf16x4*>(at) = h;
+                    *reinterpret_cast<bf16x4*>(at + 1024) = l;
+                } else {
+                    *reinterpret_cast<float4*>(p.y + static_cast<int64_t>(m) * p.ldy + f) =
+                        make_float4(o[0], o[1], o[2], o[3]);
+                }
             }
         }
     } else {

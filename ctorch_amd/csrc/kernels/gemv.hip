@@ -212,6 +212,10 @@ extern "C" int dlk_gemv(const dlk_gemv_params* params, dlh_stream stream_handle)
     if (params->epilogue == DLK_EPI_QKV)
         for (int s = 0; s < params->nseg; ++s)
             if (params->seg_rows[s] % 2 != 0 || params->head_dim % 2 != 0) return static_cast<int>(hipErrorInvalidValue);
+    // the staged SwiGLU output exists only on the tiled path
+    if (params->stage_out && (params->epilogue != DLK_EPI_SWIGLU || !dlk::tiles::eligible(*params) ||
+                              params->seg_rows[0] % 32 != 0 || reinterpret_cast<uintptr_t>(params->stage_out) % 16 != 0))
+        return static_cast<int>(hipErrorInvalidValue);
     if (dlk::tiles::eligible(*params)) return launch_tiles(*params, stream);
     if (dlk::gemm::eligible(*params)) return launch_gemm(*params, stream);
     const int waves = launch_waves(*params);

@@ -91,6 +91,9 @@ typedef struct dlk_gemv_params {
     void* stage;
     int64_t stage_bytes;
     int stage_ready;        /* the workspace already holds this launch's split rows (same x, norm weight, M, K) */
+    void* stage_out;        /* SWIGLU on the tiled path: write silu(gate) * up, split into bf16 hi + lo, in the
+                               staging layout of a following tiled launch over these rows (K = seg_rows[0]) instead
+                               of y; that launch then takes it as its stage with stage_ready set */
 } dlk_gemv_params;
 
 /* Floats of workspace that lets dlk_gemv split the keys of this launch (0 when it would not split). */

@@ -223,7 +223,26 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         });
     }
 
-    // 5. gate/up projection: fused RMSNorm prologue and SiLU(gate) * up epilogue
+    // 5. gate/up projection: fused RMSNorm prologue and SiLU(gate) * up epilogue; 6. down projection + residual.
+    // Workspaces are attached down, gate/up, down: a buffer grows only when a launch needs more than it holds, so
+    // after the first two both launches' needs are met and the last attach hands the down launch current
+    // pointers without moving the gate/up launch's.  When both take the tiled (prefill) path, gate/up writes its
+    // rows already split for the down launch, which then skips its own split pass.
+    dlk_gemv_params down{};
+    {
+        int db = 0;
+        dlk_gemv_params p = gemv_params(ws.activation.data<float>(), rows, F, DLK_EPI_RESIDUAL);
+        p.nseg = 1;
+        p.w[0] = weight_data(ff.down().weight(), db, "down");
+        p.seg_rows[0] = static_cast<int>(d);
+        p.w_bf16 = db;
+        p.y = x_out;
+        p.ldy = d;
+        p.residual = ws.hidden.data<float>();
+        p.ldres = d;
+        ws.attach_workspace(p, device);
+        down = p;
+    }
     {
         int gb = 0, ub = 0, nb = 0;
         dlk_gemv_params p = gemv_params(ws.hidden.data<float>(), rows, d, DLK_EPI_SWIGLU);
@@ -240,26 +259,21 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         p.y = static_cast<float*>(mutable_data(ws.activation));
         p.ldy = F;
         ws.attach_workspace(p, device);
+        ws.attach_workspace(down, device);
+        const int64_t down_stage = dlk_gemv_stage_bytes(&down);
+        if (p.stage && dlk_gemv_stage_bytes(&p) > 0 && down.stage && down_stage > 0 && F % 32 == 0) {
+            if (!ws.stage_ffn.defined() || ws.stage_ffn.numel() * 4 < down_stage || !(ws.stage_ffn.device() == device))
+                ws.stage_ffn = empty_tensor({(down_stage + 3) / 4}, DType::f32, device);
+            p.stage_out = mutable_data(ws.stage_ffn);
+            down.stage = p.stage_out;
+            down.stage_bytes = ws.stage_ffn.numel() * 4;
+            down.stage_ready = 1;
+        }
         issue(observer, "gate_up_silu", static_cast<double>(2 * F * d) * (gb ? 2 : 4),
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "gate/up projection"); });
     }
-
-    // 6. down projection + residual
-    {
-        int db = 0;
-        dlk_gemv_params p = gemv_params(ws.activation.data<float>(), rows, F, DLK_EPI_RESIDUAL);
-        p.nseg = 1;
-        p.w[0] = weight_data(ff.down().weight(), db, "down");
-        p.seg_rows[0] = static_cast<int>(d);
-        p.w_bf16 = db;
-        p.y = x_out;
-        p.ldy = d;
-        p.residual = ws.hidden.data<float>();
-        p.ldres = d;
-        ws.attach_workspace(p, device);
-        issue(observer, "down_residual", static_cast<double>(F * d) * (db ? 2 : 4),
-              [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "down projection"); });
-    }
+    issue(observer, "down_residual", static_cast<double>(F * d) * (down.w_bf16 ? 2 : 4),
+          [p = down, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "down projection"); });
     cache.advance(length);
 }
 
