@@ -398,6 +398,13 @@ extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stre
     if (p.B <= 0 || p.L <= 0 || p.KV <= 0 || p.H % p.KV != 0 || p.splits <= 0 || p.chunk <= 0 ||
         (p.splits > 1 && (!p.partial_o || !p.partial_ml)) || (p.splits > 1 && p.chunk % 64 != 0))
         return static_cast<int>(hipErrorInvalidValue);
+    // the staged output exists only on the prefill kernel
+    if (p.stage_out) {
+        if (!dlk_attention_prefill_eligible(&p) || (p.H * p.hd) % 32 != 0 ||
+            reinterpret_cast<uintptr_t>(p.stage_out) % 16 != 0)
+            return static_cast<int>(hipErrorInvalidValue);
+        return dlk_attention_prefill(&p, stream_handle);
+    }
     // one position on the matrix cores, then the merge of its key splits
     if (dlk_attention_matrix_eligible(&p)) {
         const int status = dlk_attention_matrix_decode(&p, stream_handle);

@@ -339,12 +339,30 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
     for (int tile = 0; tile < min(unmasked, tiles); ++tile) step(tile, std::false_type{});
     for (int tile = unmasked; tile < tiles; ++tile) step(tile, std::true_type{});
 
-    // lane holds O[query row (qt, lane % 16)][d = 16 dt + 4 q + j]
+    // lane holds O[query row (qt, lane % 16)][d = 16 dt + 4 q + j].  With stage_out the four values go to the
+    // projection's staging layout instead (row m = b L + l, k = head HD + d): hi and lo of row m, k step k / 32,
+    // lane (m % 16) + 16 ((k % 32) / 8), elements k % 8 .. +4, the split its preparation pass would make
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         if (!valid[qt]) continue;
         const float inv = 1.0f / l[qt][0];
-        float* out = p.out + (static_cast<int64_t>(b) * p.L + pos[qt]) * p.ldo + static_cast<int64_t>(head[qt]) * HD;
+        const int64_t row = static_cast<int64_t>(b) * p.L + pos[qt];
+        if (p.stage_out) {
+            const int ksteps = p.H * HD / 32;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int k = head[qt] * HD + 16 * dt + 4 * q;
+                const f32x4 v = {o[qt][dt][0] * inv, o[qt][dt][1] * inv, o[qt][dt][2] * inv, o[qt][dt][3] * inv};
+                const bf16x4 h = __builtin_convertvector(v, bf16x4);
+                const bf16x4 lo = __builtin_convertvector(v - __builtin_convertvector(h, f32x4), bf16x4);
+                char* at = static_cast<char*>(p.stage_out) + ((row / 16) * ksteps + k / 32) * 2048 +
+                           ((row % 16) + 16 * ((k % 32) / 8)) * 16 + (k % 8) * 2;
+                *reinterpret_cast<bf16x4*>(at) = h;
+                *reinterpret_cast<bf16x4*>(at + 1024) = lo;
+            }
+            continue;
+        }
+        float* out = p.out + row * p.ldo + static_cast<int64_t>(head[qt]) * HD;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
             *reinterpret_cast<float4*>(out + 16 * dt + 4 * q) =

@@ -134,6 +134,9 @@ typedef struct dlk_attention_params {
     float* partial_o;        /* [B*H*L, splits, hd] */
     float* partial_ml;       /* [B*H*L, splits, 2] */
     int partials_only;       /* splits > 1: leave the merge of the partials to the caller (no combine launch) */
+    void* stage_out;         /* prefill kernel only: write the output rows (row b * L + l, K = H * hd) split into
+                                bf16 hi + lo in the staging layout of the tiled projection that reads them, instead
+                                of out (see dlk_gemv_params.stage_out) */
 } dlk_attention_params;
 
 /* Keys per split of a short one-position decode over a bf16 cache (few keys in all): 256 or 512, one work-group. */

@@ -174,6 +174,26 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "QKV projection"); });
     }
 
+    // 4's parameters first: when the output projection takes the tiled (prefill) path and the attention the
+    // prefill kernel, the attention writes its rows already split for the projection, which skips its split pass
+    dlk_gemv_params out{};
+    {
+        int ob = 0;
+        dlk_gemv_params p = gemv_params(ws.attention.data<float>(), rows, d, DLK_EPI_RESIDUAL);
+        p.nseg = 1;
+        p.w[0] = weight_data(attention.output().weight(), ob, "output projection");
+        p.seg_rows[0] = static_cast<int>(d);
+        p.w_bf16 = ob;
+        p.y = static_cast<float*>(mutable_data(ws.hidden));
+        p.ldy = d;
+        p.residual = x_in;
+        p.ldres = d;
+        p.bump_position = cache.position_data();
+        p.bump_count = length;
+        ws.attach_workspace(p, device);
+        out = p;
+    }
+
     // 3. split-K attention over the cache (reads the device length, sees the keys just appended)
     {
         dlk_attention_params a{};
@@ -196,32 +216,26 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
             a.partial_o = static_cast<float*>(mutable_data(ws.partial_o));
             a.partial_ml = static_cast<float*>(mutable_data(ws.partial_ml));
         }
+        const int64_t out_stage = dlk_gemv_stage_bytes(&out);
+        if (out.stage && out_stage > 0 && dlk_attention_prefill_eligible(&a) && (H * hd) % 32 == 0) {
+            if (!ws.stage_attn.defined() || ws.stage_attn.numel() * 4 < out_stage || !(ws.stage_attn.device() == device))
+                ws.stage_attn = empty_tensor({(out_stage + 3) / 4}, DType::f32, device);
+            a.stage_out = mutable_data(ws.stage_attn);
+            out.stage = a.stage_out;
+            out.stage_bytes = ws.stage_attn.numel() * 4;
+            out.stage_ready = 1;
+        }
         const double bytes = 2.0 * kv_bytes_per * static_cast<double>(cache.length() + length);
         issue(observer, "attention", bytes,
               [a, &context](bool) { hip_check(dlk_attention(&a, context.stream), "attention"); });
     }
 
     // 4. output projection + residual; advances the device cache length by `length`
-    {
-        int ob = 0;
-        dlk_gemv_params p = gemv_params(ws.attention.data<float>(), rows, d, DLK_EPI_RESIDUAL);
-        p.nseg = 1;
-        p.w[0] = weight_data(attention.output().weight(), ob, "output projection");
-        p.seg_rows[0] = static_cast<int>(d);
-        p.w_bf16 = ob;
-        p.y = static_cast<float*>(mutable_data(ws.hidden));
-        p.ldy = d;
-        p.residual = x_in;
-        p.ldres = d;
-        p.bump_position = cache.position_data();
-        p.bump_count = length;
-        ws.attach_workspace(p, device);
-        issue(observer, "output_residual", static_cast<double>(d * d) * (ob ? 2 : 4), [p, &context](bool repeat) {
-            dlk_gemv_params q = p;
-            if (repeat) q.bump_position = nullptr; // a timing repeat leaves the device length alone
-            hip_check(dlk_gemv(&q, context.stream), "output projection");
-        });
-    }
+    issue(observer, "output_residual", static_cast<double>(d * d) * (out.w_bf16 ? 2 : 4), [p = out, &context](bool repeat) {
+        dlk_gemv_params q = p;
+        if (repeat) q.bump_position = nullptr; // a timing repeat leaves the device length alone
+        hip_check(dlk_gemv(&q, context.stream), "output projection");
+    });
 
     // 5. gate/up projection: fused RMSNorm prologue and SiLU(gate) * up epilogue; 6. down projection + residual.
     // Workspaces are attached down, gate/up, down: a buffer grows only when a launch needs more than it holds, so

@@ -18,6 +18,7 @@ struct DecodeWorkspace {
     Tensor lora; ///< LoRA hidden rows [rows, rank_q + rank_v]: the query adapter's, then the value adapter's
     Tensor split; ///< key-split partials of the matrix-core projections (shared: launches are stream-ordered)
     Tensor stage_ffn; ///< prefill: the SwiGLU rows already split for the down projection's tiled path
+    Tensor stage_attn; ///< prefill: the attention rows already split for the output projection's tiled path
     Tensor stage; ///< prefill projections: activation rows split into bf16 hi + lo, per-row norm factors
     /// Points `p` at the staging workspace when its shape takes the tiled prefill path and at the split
     /// workspace when its launch would split the keys (both grown as needed).
