@@ -398,6 +398,8 @@ extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stre
     if (p.B <= 0 || p.L <= 0 || p.KV <= 0 || p.H % p.KV != 0 || p.splits <= 0 || p.chunk <= 0 ||
         (p.splits > 1 && (!p.partial_o || !p.partial_ml)) || (p.splits > 1 && p.chunk % 64 != 0))
         return static_cast<int>(hipErrorInvalidValue);
+    // the QKV projection's partials are finished only by the matrix kernel
+    if (p.qkv_partial && (p.stage_out || !dlk_attention_matrix_eligible(&p))) return static_cast<int>(hipErrorInvalidValue);
     // the staged output exists only on the prefill kernel
     if (p.stage_out) {
         if (!dlk_attention_prefill_eligible(&p) || (p.H * p.hd) % 32 != 0 ||

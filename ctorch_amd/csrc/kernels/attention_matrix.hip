@@ -86,6 +86,7 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
     __shared__ __attribute__((aligned(16))) uint16_t vt[W][PLANES][HD * VSTRIDE];
     __shared__ float m_s[W][16], l_s[W][16];
     __shared__ float o_s[W][16][HD];
+    __shared__ __attribute__((aligned(16))) float kv_s[2][HD]; // the new K/V row (qkv_partial holder wave)
 
     const int t = threadIdx.x, lane = t % kWave, q = lane / 16, col = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
@@ -110,19 +111,9 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
     const int keys = static_cast<int>(max<int64_t>(0, min<int64_t>(k_end, w_begin + per_wave) - w_begin));
     const int tiles = (keys + kTileKeys - 1) / kTileKeys;
 
-    // the query heads of this KV head as the B operand (column col = head kvh G + col), scaled into base 2
+    // the query heads of this KV head as the B operand (column col = head kvh G + col), scaled into base 2; set
+    // below, after the first K/V tile is requested
     bf16x8 qh[KS], ql[KS];
-    {
-        const float qs = p.scale * 1.4426950408889634f;
-        const float* qrow = p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G + min(col, G - 1)) * HD;
-#pragma unroll
-        for (int st = 0; st < KS; ++st) {
-            const float4 a = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q);
-            const float4 c = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q + 4);
-            const float z = col < G ? qs : 0.0f;
-            split8(f32x8{a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w} * z, qh[st], ql[st]);
-        }
-    }
 
     // buffer ranges over this wave's keys: rows past them read as zero
     const size_t head = (static_cast<size_t>(b) * p.KV + kvh) * p.capacity + w_begin;
@@ -261,18 +252,166 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
             }
         }
     };
+    // The QKV projection's partials, when the projection left them (qkv_partial): every wave finishes the query
+    // rows of its KV head's G heads from them, in the projection's reduce order (slices in order, the RMSNorm
+    // factor from the summed row squares, RoPE on interleaved pairs at the new position), staged through its own
+    // part of o_s (free until the merge).  The one wave whose keys hold the new position (in the last active
+    // split's work-group) also finishes the new K/V row: it writes the row into the cache for later steps and
+    // puts it in place of what its tile load returned for that key, so no wave waits on the write.
+    const bool finish = p.qkv_partial != nullptr;
+    const int64_t newest = S - 1;
+    const bool holder = finish && split == active - 1 && newest >= w_begin && newest < w_begin + keys;
+    const int patch_tile = holder ? static_cast<int>(newest - w_begin) / kTileKeys : -1;
+    const int patch_key = holder ? static_cast<int>(newest - w_begin) % kTileKeys : 0;
+    Tile a, c;
+    if (tiles > 0) load(0, a);
+    {
+        const float qs = p.scale * 1.4426950408889634f;
+        const float z = col < G ? qs : 0.0f;
+        const float* qrow;
+        if (finish) {
+            constexpr int kBatch = 8; // slices requested at once
+            constexpr int UNITS = HD / 4; // 4-dim units per head row
+            const int width = p.qkv_width;
+            const int slice = p.B * width; // floats per slice
+            const __amdgpu_buffer_rsrc_t dots = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(p.qkv_partial), 0, p.qkv_splits * slice * 4, kBufferFlags);
+            float f = p.qkv_scale;
+            if (p.qkv_norm) {
+                const __amdgpu_buffer_rsrc_t sums = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<float*>(p.qkv_partial) + static_cast<int64_t>(p.qkv_splits) * slice, 0,
+                    p.qkv_splits * p.B * 4, kBufferFlags);
+                float row[16];
+#pragma unroll
+                for (int s = 0; s < 16; ++s)
+                    row[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(sums, (s * p.B + b) * 4, 0, 0));
+                float total = 0.0f;
+#pragma unroll
+                for (int s = 0; s < 16; ++s) total += row[s];
+                f = rsqrtf(total / static_cast<float>(p.qkv_K) + p.qkv_epsilon) * p.qkv_scale;
+            }
+            const float* cosine = p.rope_cos + newest * (HD / 2);
+            const float* sine = p.rope_sin + newest * (HD / 2);
+            float* stage = &o_s[wave][0][0];
+            const int qunits = G * UNITS;
+            // round r: lane finishes query unit lane + 64 r (head g, dims d .. +4) and, in round 0 of the holder,
+            // K/V unit lane (lanes < UNITS: key dims 4 lane .., then value dims)
+            for (int r = 0; r * kWave < qunits; ++r) {
+                const int unit = min(lane + kWave * r, qunits - 1);
+                const int g = unit / UNITS, d = 4 * (unit % UNITS);
+                const int qoff = (b * width + (kvh * G + g) * HD + d) * 4;
+                const bool kv = holder && r == 0 && lane < 2 * UNITS;
+                const bool key = lane < UNITS;
+                const int kd = 4 * (lane % UNITS);
+                const int koff = (b * width + p.H * HD + (key ? 0 : p.KV * HD) + kvh * HD + kd) * 4;
+                f32x4 qa = f32x4{0.f, 0.f, 0.f, 0.f}, ka = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int s0 = 0; s0 < p.qkv_splits; s0 += kBatch) {
+                    u32x4 qp[kBatch], kp[kBatch];
+#pragma unroll
+                    for (int s = 0; s < kBatch; ++s)
+                        qp[s] = __builtin_amdgcn_raw_buffer_load_b128(dots, qoff + (s0 + s) * slice * 4, 0, 0);
+                    if (kv) {
+#pragma unroll
+                        for (int s = 0; s < kBatch; ++s)
+                            kp[s] = __builtin_amdgcn_raw_buffer_load_b128(dots, koff + (s0 + s) * slice * 4, 0, 0);
+                    }
+#pragma unroll
+                    for (int s = 0; s < kBatch; ++s) qa += __builtin_bit_cast(f32x4, qp[s]);
+                    if (kv) {
+#pragma unroll
+                        for (int s = 0; s < kBatch; ++s) ka += __builtin_bit_cast(f32x4, kp[s]);
+                    }
+                }
+                // RoPE: even' = e c - o s, odd' = e s + o c on the pairs (d, d + 1), (d + 2, d + 3)
+                const float2 qc = *reinterpret_cast<const float2*>(cosine + d / 2);
+                const float2 qs2 = *reinterpret_cast<const float2*>(sine + d / 2);
+                qa *= f;
+                const f32x4 qr = f32x4{qa[0] * qc.x - qa[1] * qs2.x, qa[0] * qs2.x + qa[1] * qc.x,
+                                       qa[2] * qc.y - qa[3] * qs2.y, qa[2] * qs2.y + qa[3] * qc.y};
+                if (lane + kWave * r < qunits) *reinterpret_cast<f32x4*>(stage + g * HD + d) = qr;
+                if (kv) {
+                    ka *= f;
+                    f32x4 kr = ka;
+                    if (key) {
+                        const float2 kc = *reinterpret_cast<const float2*>(cosine + kd / 2);
+                        const float2 ks = *reinterpret_cast<const float2*>(sine + kd / 2);
+                        kr = f32x4{ka[0] * kc.x - ka[1] * ks.x, ka[0] * ks.x + ka[1] * kc.x,
+                                   ka[2] * kc.y - ka[3] * ks.y, ka[2] * ks.y + ka[3] * kc.y};
+                    }
+                    const int64_t index = ((static_cast<int64_t>(b) * p.KV + kvh) * p.capacity + newest) * HD + kd;
+                    KT* dst = const_cast<KT*>(static_cast<const KT*>(key ? p.k : p.v)) + index;
+                    if constexpr (F32) {
+                        *reinterpret_cast<f32x4*>(dst) = kr;
+                    } else {
+                        // the cache's bf16 values, and the same values for the patch below
+                        *reinterpret_cast<u32x2*>(dst) =
+                            u32x2{static_cast<uint32_t>(f32_to_bf16(kr[0])) | (static_cast<uint32_t>(f32_to_bf16(kr[1])) << 16),
+                                  static_cast<uint32_t>(f32_to_bf16(kr[2])) | (static_cast<uint32_t>(f32_to_bf16(kr[3])) << 16)};
+                    }
+                    *reinterpret_cast<f32x4*>(&kv_s[key ? 0 : 1][kd]) = kr;
+                }
+            }
+            // the staged rows are read back by the lanes of this wave only (LDS operations of a wave complete in
+            // order); the barrier keeps the compiler from moving the reads above the writes
+            __asm__ volatile("" ::: "memory");
+            qrow = stage + min(col, G - 1) * HD;
+        } else {
+            qrow = p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G + min(col, G - 1)) * HD;
+        }
+#pragma unroll
+        for (int st = 0; st < KS; ++st) {
+            const float4 x0 = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q);
+            const float4 x1 = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q + 4);
+            split8(f32x8{x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w} * z, qh[st], ql[st]);
+        }
+        __asm__ volatile("" ::: "memory");
+    }
+    // The holder's new key in its tile's registers (K: lanes col = key % 16 of half key / 16 hold dims
+    // 32 st + 8 q ..; V: lanes col = key / 2, member key % 2 hold pieces q + 4 i), in the cache's type.
+    auto to_kt = [&](const float* src) -> u32x4 {
+        if constexpr (F32) {
+            return __builtin_bit_cast(u32x4, *reinterpret_cast<const f32x4*>(src));
+        } else {
+            u32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = static_cast<uint32_t>(f32_to_bf16(src[2 * e])) |
+                       (static_cast<uint32_t>(f32_to_bf16(src[2 * e + 1])) << 16);
+            return w;
+        }
+    };
+    auto patch = [&](int tile, Tile& dst) {
+        if (tile != patch_tile) return;
+        __asm__ volatile("" ::: "memory"); // the row is read here, not kept in registers through the loop
+        const int u = patch_key / 16, kc = patch_key % 16, vc = patch_key / 2, ve = patch_key % 2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int st = 0; st < KS; ++st)
+#pragma unroll
+                for (int e = 0; e < KL; ++e) {
+                    const u32x4 w = to_kt(&kv_s[0][32 * st + 8 * q + e * DPP]);
+                    if (h == u && col == kc) dst.k[h][st][e] = w;
+                }
+#pragma unroll
+        for (int i = 0; i < VI; ++i)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const u32x4 w = to_kt(&kv_s[1][DPP * (q + 4 * i)]);
+                if (e == ve && col == vc) dst.v[i][e] = w;
+            }
+    };
     if (tiles > 0) {
-        Tile a, c;
-        load(0, a);
         // two tiles per iteration so that the buffers are named statically; the next tile is in flight while one
-        // is used, and no load sits in a branch inside the loop (the last tile is peeled)
+        // is used, and no load sits in a branch inside the loop (the last tile is peeled: the new key, the last
+        // of its range, is always in the holder's last tile)
         int tile = 0;
         for (;;) {
-            if (tile + 1 >= tiles) { use(tile, a); break; }
+            if (tile + 1 >= tiles) { patch(tile, a); use(tile, a); break; }
             load(tile + 1, c);
             use(tile, a);
             ++tile;
-            if (tile + 1 >= tiles) { use(tile, c); break; }
+            if (tile + 1 >= tiles) { patch(tile, c); use(tile, c); break; }
             load(tile + 1, a);
             use(tile, c);
             ++tile;
@@ -346,8 +485,13 @@ extern "C" int dlk_attention_matrix_heads(int heads, int kv_heads, int head_dim)
 /* Whether dlk_attention_matrix_decode takes these parameters: one position, head dim 64 or 128, at most 16 query
    heads per KV head, key chunks of whole 32-key tiles per wave. */
 extern "C" int dlk_attention_matrix_eligible(const dlk_attention_params* p) {
+    // the partials are addressed with 32-bit byte offsets (batches of 8 slices run up to 24 slices past the base)
+    const bool qkv = !p->qkv_partial ||
+                     (p->qkv_splits >= 1 && p->qkv_splits <= 16 && p->rope_cos && p->rope_sin && p->qkv_K > 0 &&
+                      p->qkv_width == (p->H + 2 * p->KV) * p->hd &&
+                      24LL * p->B * p->qkv_width * 4 <= INT32_MAX);
     return p->L == 1 && dlk_attention_matrix_heads(p->H, p->KV, p->hd) && p->chunk % (4 * dlk::kTileKeys) == 0 &&
-           p->ldq % 4 == 0 &&
+           p->ldq % 4 == 0 && qkv &&
            (p->splits == 1 || (p->partial_o && p->partial_ml));
 }
 

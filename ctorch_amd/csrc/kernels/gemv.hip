@@ -114,6 +114,9 @@ int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
         if (splits > 1 && (!p.split_partial || p.split_capacity < split_floats(p, splits, p.M))) splits = 1;
         // the reduce addresses the partials with 32-bit byte offsets
         if (splits > 1 && split_floats(p, kMaxSplits, p.M) * 4 > INT32_MAX) splits = 1;
+        // a deferred reduce leaves one row block's QKV partials for the attention
+        if (p.defer_reduce && (splits == 1 || p.epilogue != DLK_EPI_QKV || params.M > kMaxRows))
+            return static_cast<int>(hipErrorInvalidValue);
         const int mt = row_tiles(p.M);
         const Kernel kernel = resolve_gemm(p, mt, upfront_chunks(p.K / splits / chunk_k(mt)));
         if (!kernel.fn) return static_cast<int>(hipErrorInvalidValue);
@@ -122,6 +125,7 @@ int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
         void* args[] = {&p};
         hipError_t status = hipLaunchKernel(kernel.fn, dim3(blocks, splits), dim3(kThreads), args, kernel.lds, stream);
         if (status != hipSuccess) return static_cast<int>(status);
+        if (p.defer_reduce) continue; // the attention finishes the projection
         if (splits > 1) {
             p.bump_position = const_cast<int64_t*>(bump);
             const Kernel reduce = resolve_reduce(p);
@@ -187,6 +191,15 @@ extern "C" int64_t dlk_gemv_split_floats(const dlk_gemv_params* p) {
     return dlk::gemm::split_floats(*p, dlk::gemm::splits_of(*p, rows), rows);
 }
 
+extern "C" int dlk_gemv_split_count(const dlk_gemv_params* p) {
+    using namespace dlk::gemm;
+    if (dlk::tiles::eligible(*p) || !eligible(*p) || p->M > kMaxRows || wide_eligible(*p)) return 1;
+    int splits = splits_of(*p, p->M);
+    if (splits > 1 && (!p->split_partial || p->split_capacity < split_floats(*p, splits, p->M))) splits = 1;
+    if (splits > 1 && split_floats(*p, kMaxSplits, p->M) * 4 > INT32_MAX) splits = 1;
+    return splits;
+}
+
 extern "C" int64_t dlk_gemv_stage_bytes(const dlk_gemv_params* p) {
     return dlk::tiles::shape_eligible(*p) ? dlk::tiles::stage_bytes(*p) : 0;
 }
@@ -215,6 +228,9 @@ extern "C" int dlk_gemv(const dlk_gemv_params* params, dlh_stream stream_handle)
     // the staged SwiGLU output exists only on the tiled path
     if (params->stage_out && (params->epilogue != DLK_EPI_SWIGLU || !dlk::tiles::eligible(*params) ||
                               params->seg_rows[0] % 32 != 0 || reinterpret_cast<uintptr_t>(params->stage_out) % 16 != 0))
+        return static_cast<int>(hipErrorInvalidValue);
+    if (params->defer_reduce && (dlk::tiles::eligible(*params) || !dlk::gemm::eligible(*params) ||
+                                 dlk::gemm::wide_eligible(*params)))
         return static_cast<int>(hipErrorInvalidValue);
     if (dlk::tiles::eligible(*params)) return launch_tiles(*params, stream);
     if (dlk::gemm::eligible(*params)) return launch_gemm(*params, stream);

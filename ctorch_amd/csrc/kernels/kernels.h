@@ -91,6 +91,8 @@ typedef struct dlk_gemv_params {
     void* stage;
     int64_t stage_bytes;
     int stage_ready;        /* the workspace already holds this launch's split rows (same x, norm weight, M, K) */
+    int defer_reduce;       /* QKV on the key-split matrix-core path: leave the partials for the one-position
+                               attention to finish (no reduce launch); see dlk_attention_params.qkv_partial */
     void* stage_out;        /* SWIGLU on the tiled path: write silu(gate) * up, split into bf16 hi + lo, in the
                                staging layout of a following tiled launch over these rows (K = seg_rows[0]) instead
                                of y; that launch then takes it as its stage with stage_ready set */
@@ -98,6 +100,8 @@ typedef struct dlk_gemv_params {
 
 /* Floats of workspace that lets dlk_gemv split the keys of this launch (0 when it would not split). */
 int64_t dlk_gemv_split_floats(const dlk_gemv_params* p);
+/* Key slices dlk_gemv will use for this launch as attached (1: no split). */
+int dlk_gemv_split_count(const dlk_gemv_params* p);
 /* Bytes of staging workspace that lets this launch take the tiled (prefill) path: attach it as stage /
    stage_bytes (0 when the shape does not suit that path). */
 int64_t dlk_gemv_stage_bytes(const dlk_gemv_params* p);
@@ -134,6 +138,16 @@ typedef struct dlk_attention_params {
     float* partial_o;        /* [B*H*L, splits, hd] */
     float* partial_ml;       /* [B*H*L, splits, 2] */
     int partials_only;       /* splits > 1: leave the merge of the partials to the caller (no combine launch) */
+    /* One position on the matrix-core kernel: the QKV projection's key-split partials, left unreduced by it
+       (dlk_gemv_params.defer_reduce).  The attention sums them in slice order for its sequence's q, k and v
+       columns, applies the RMSNorm factor (row sums of squares after the dots) and RoPE at *position, and writes
+       the new K/V row into the cache at *position before reading the keys.  Layout: [qkv_splits][B][qkv_width]
+       dot products (q columns, then k, then v), then [qkv_splits][B] sums of squares. */
+    const float* qkv_partial;
+    int qkv_splits, qkv_width, qkv_K, qkv_norm;
+    float qkv_scale, qkv_epsilon;
+    const float* rope_cos;   /* [capacity, hd/2] */
+    const float* rope_sin;
     void* stage_out;         /* prefill kernel only: write the output rows (row b * L + l, K = H * hd) split into
                                 bf16 hi + lo in the staging layout of the tiled projection that reads them, instead
                                 of out (see dlk_gemv_params.stage_out) */

@@ -120,7 +120,9 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "LoRA down projection"); });
     }
 
-    // 2. QKV projection: fused RMSNorm prologue, (LoRA,) RoPE and KV append epilogue
+    // 2. QKV projection: fused RMSNorm prologue, (LoRA,) RoPE and KV append epilogue; issued with the attention
+    dlk_gemv_params qkv{};
+    double qkv_bytes = 0.0;
     {
         int qb = 0, kb = 0, vb = 0, nb = 0;
         dlk_gemv_params p = gemv_params(x_in, rows, d, DLK_EPI_QKV);
@@ -167,11 +169,9 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
             (attention.query_adapter()->rank() != attention.value_adapter()->rank() ||
              attention.query_adapter()->scale() != attention.value_adapter()->scale()))
             throw std::invalid_argument("query and value adapters must share rank and alpha");
-        const double bytes = static_cast<double>((H + 2 * KV) * hd * d) * (qb ? 2 : 4) + 2.0 * kv_bytes_per * length;
+        qkv_bytes = static_cast<double>((H + 2 * KV) * hd * d) * (qb ? 2 : 4) + 2.0 * kv_bytes_per * length;
         ws.attach_workspace(p, device);
-        share_stage(p);
-        issue(observer, "qkv_rope_append", bytes,
-              [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "QKV projection"); });
+        qkv = p;
     }
 
     // 4's parameters first: when the output projection takes the tiled (prefill) path and the attention the
@@ -193,6 +193,10 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         ws.attach_workspace(p, device);
         out = p;
     }
+    // the output projection's attach may have grown the split buffer: the QKV launch takes the current one (the
+    // attention may read its partials), which already fits both launches
+    ws.attach_workspace(qkv, device);
+    share_stage(qkv);
 
     // 3. split-K attention over the cache (reads the device length, sees the keys just appended)
     {
@@ -225,6 +229,34 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
             out.stage_bytes = ws.stage_attn.numel() * 4;
             out.stage_ready = 1;
         }
+        // One new position without adapters, when the projection splits its keys and the attention's work-groups
+        // fit one per CU: the attention finishes the projection from its partials (sums them, normalises,
+        // rotates, appends K/V), which drops the reduce launch.  Every work-group pays the partials' round trip
+        // before its first tile, so a grid of several work-groups per CU (MI355X, 8B at b=8 over 32768 keys:
+        // 10.2 -> 10.8 ms a step) keeps the reduce launch; at one per CU (1B at b=32: 1.49 -> 1.45 ms) it pays.
+        const bool one_per_cu = static_cast<int64_t>(a.splits) * batch * KV <= 256;
+        const int qkv_splits = length == 1 && !adapters[0] && !adapters[1] && !a.stage_out && one_per_cu
+                                   ? dlk_gemv_split_count(&qkv)
+                                   : 1;
+        if (qkv_splits > 1) {
+            dlk_attention_params f = a;
+            f.qkv_partial = qkv.split_partial;
+            f.qkv_splits = qkv_splits;
+            f.qkv_width = static_cast<int>((H + 2 * KV) * hd);
+            f.qkv_K = static_cast<int>(d);
+            f.qkv_norm = qkv.apply_norm;
+            f.qkv_scale = qkv.acc_scale;
+            f.qkv_epsilon = qkv.epsilon;
+            f.rope_cos = qkv.cosine;
+            f.rope_sin = qkv.sine;
+            if (dlk_attention_matrix_eligible(&f)) {
+                a = f;
+                qkv.defer_reduce = 1;
+            }
+        }
+        // the label names what the launch leaves: finished rows, or the partials the attention finishes
+        issue(observer, qkv.defer_reduce ? "qkv_split" : "qkv_rope_append", qkv_bytes,
+              [p = qkv, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "QKV projection"); });
         const double bytes = 2.0 * kv_bytes_per * static_cast<double>(cache.length() + length);
         issue(observer, "attention", bytes,
               [a, &context](bool) { hip_check(dlk_attention(&a, context.stream), "attention"); });

@@ -245,6 +245,8 @@ def test_batched_decode_on_matrix_cores():
         got = gpu.logits(ids, gc)
         assert np.max(np.abs(got - want)) <= 2e-2, step
         ids = want.argmax(-1).reshape(B, 1)
+    # those steps took the route where the attention finishes the key-split QKV projection (no reduce launch)
+    assert "qkv_split" in {x["name"] for x in gpu.lm.profile(ids, gc, 1)}
     t1, l1 = gpu.generate(prompt, 10, 1.0, (3, 4), use_graph=True)
     t2, l2 = gpu.generate(prompt, 10, 1.0, (3, 4), use_graph=False)
     assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
@@ -269,6 +271,8 @@ def test_head_dim_128_batched_decode_over_a_long_prefix(kv):
         got = gpu.logits(ids, gc)
         assert np.max(np.abs(got - want)) <= 2e-2, step
         ids = want.argmax(-1).reshape(B, 1)
+    # 4 key splits of 16 (sequence, KV head) pairs: the attention finishes the key-split QKV projection
+    assert "qkv_split" in {x["name"] for x in gpu.lm.profile(ids, gc, 1)}
     gc.truncate(P)
     t1, l1 = gpu.generate(ids, 6, 0.0, (0, 0), use_graph=True, cache=gc)
     gc.truncate(P)
