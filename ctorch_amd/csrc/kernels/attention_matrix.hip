@@ -105,9 +105,13 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
         }
         return;
     }
-    const int per_wave = p.chunk / W;
-    const int64_t k_end = min(S, static_cast<int64_t>(split) * p.chunk + p.chunk);
-    const int64_t w_begin = static_cast<int64_t>(split) * p.chunk + static_cast<int64_t>(wave) * per_wave;
+    // the split's live keys in equal runs of whole tiles per wave (a split past most of the sequence's keys, or
+    // a chunk sized for a longer sequence, keeps every wave busy for fewer tiles)
+    const int64_t s_begin = static_cast<int64_t>(split) * p.chunk;
+    const int64_t k_end = min(S, s_begin + p.chunk);
+    const int live = static_cast<int>(k_end - s_begin);
+    const int per_wave = ((live + W - 1) / W + kTileKeys - 1) / kTileKeys * kTileKeys;
+    const int64_t w_begin = s_begin + static_cast<int64_t>(wave) * per_wave;
     const int keys = static_cast<int>(max<int64_t>(0, min<int64_t>(k_end, w_begin + per_wave) - w_begin));
     const int tiles = (keys + kTileKeys - 1) / kTileKeys;
 
