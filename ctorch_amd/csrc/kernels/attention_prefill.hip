@@ -83,9 +83,86 @@ __device__ __forceinline__ void split4(const u32x4 w, u32x2& hi, u32x2& lo) {
     lo = __builtin_bit_cast(u32x2, __builtin_convertvector(v - back, bf16x4));
 }
 
-template <typename KT, int HD>
+// Pre-split K/V tiles of an f32 cache: for each (sequence, KV head) and 64-key tile, the K rows and the V^T rows
+// split into bf16 hi and lo planes exactly as the attention kernel stages them in LDS (rows padded to KSTRIDE and
+// VSTRIDE; keys at or past the end zero), one tile after another: [B * KV][kv_split_tiles][K hi | K lo | V^T hi |
+// V^T lo].  One preparation pass per launch replaces the split that every work-group of a (sequence, KV head)
+// would repeat on each tile it reads (C5: 128 work-groups per pair), and the attention copies a tile into LDS
+// with the global->LDS DMA, no registers or vector-ALU work on the way.
+template <int HD> struct SplitTile {
+    static constexpr int KSTRIDE = HD + 8, VSTRIDE = kKeys + 8;
+    static constexpr int KPLANE = kKeys * KSTRIDE * 2, VPLANE = HD * VSTRIDE * 2; // bytes
+    static constexpr int BYTES = 2 * KPLANE + 2 * VPLANE;
+    static_assert(KPLANE % 1024 == 0 && VPLANE % 1024 == 0, "whole 1 KB DMA blocks");
+};
+
+// The preparation pass: work-group (tile, b * KV + kvh), the thread-to-piece maps of the kernel's own staging.
+template <int HD>
+__global__ __launch_bounds__(kThreads) void split_kv(const dlk_attention_params p) {
+    using T = SplitTile<HD>;
+    constexpr int NG = HD / 4;                  // 16-byte pieces (4 floats) per row
+    constexpr int LOADS = kKeys * NG / kThreads;
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave, kp = lane % 32;
+    const int tile = blockIdx.x, bk = blockIdx.y;
+    const int64_t S = (p.position ? *p.position : p.first_host) + p.L;
+    if (static_cast<int64_t>(tile) * kKeys >= S) return;
+    const float* kbase = static_cast<const float*>(p.k) + static_cast<int64_t>(bk) * p.capacity * HD;
+    const float* vbase = static_cast<const float*>(p.v) + static_cast<int64_t>(bk) * p.capacity * HD;
+    char* dst = static_cast<char*>(p.kv_split) + (static_cast<int64_t>(bk) * p.kv_split_tiles + tile) * T::BYTES;
+    uint16_t* khi = reinterpret_cast<uint16_t*>(dst);
+    uint16_t* klo = reinterpret_cast<uint16_t*>(dst + T::KPLANE);
+    uint16_t* vhi = reinterpret_cast<uint16_t*>(dst + 2 * T::KPLANE);
+    uint16_t* vlo = reinterpret_cast<uint16_t*>(dst + 2 * T::KPLANE + T::VPLANE);
+    u32x4 kr[LOADS], vr[LOADS];
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int c = t + kThreads * i, key = c / NG, dg = c % NG;
+        const int64_t row = static_cast<int64_t>(tile) * kKeys + key;
+        kr[i] = row < S ? *reinterpret_cast<const u32x4*>(kbase + row * HD + 4 * dg) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < LOADS / 2; ++i) {
+        const int dg = 2 * wave + lane / 32 + 8 * i;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int64_t row = static_cast<int64_t>(tile) * kKeys + 2 * kp + e;
+            vr[2 * i + e] =
+                row < S ? *reinterpret_cast<const u32x4*>(vbase + row * HD + 4 * dg) : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int c = t + kThreads * i, key = c / NG, dg = c % NG;
+        u32x2 hi, lo;
+        split4(kr[i], hi, lo);
+        *reinterpret_cast<u32x2*>(khi + key * T::KSTRIDE + 4 * dg) = hi;
+        *reinterpret_cast<u32x2*>(klo + key * T::KSTRIDE + 4 * dg) = lo;
+    }
+#pragma unroll
+    for (int i = 0; i < LOADS / 2; ++i) {
+        const int dg = 2 * wave + lane / 32 + 8 * i;
+        // key 2 kp's hi (lo) values in the low halves, key 2 kp + 1's in the high halves
+        u32x2 h0, l0, h1, l1;
+        split4(vr[2 * i], h0, l0);
+        split4(vr[2 * i + 1], h1, l1);
+        const uint32_t h[4] = {h0.x & 0xffffu, h0.x >> 16, h0.y & 0xffffu, h0.y >> 16};
+        const uint32_t hn[4] = {h1.x << 16, h1.x & 0xffff0000u, h1.y << 16, h1.y & 0xffff0000u};
+        const uint32_t l[4] = {l0.x & 0xffffu, l0.x >> 16, l0.y & 0xffffu, l0.y >> 16};
+        const uint32_t ln[4] = {l1.x << 16, l1.x & 0xffff0000u, l1.y << 16, l1.y & 0xffff0000u};
+        uint32_t* col_h = reinterpret_cast<uint32_t*>(vhi + 4 * dg * T::VSTRIDE + 2 * kp);
+        uint32_t* col_l = reinterpret_cast<uint32_t*>(vlo + 4 * dg * T::VSTRIDE + 2 * kp);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            col_h[e * (T::VSTRIDE / 2)] = h[e] | hn[e]; // head-dim 4 dg + e
+            col_l[e * (T::VSTRIDE / 2)] = l[e] | ln[e];
+        }
+    }
+}
+
+template <typename KT, int HD, bool SPLIT>
 __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_prefill(const dlk_attention_params p) {
     constexpr bool F32 = sizeof(KT) == 4;
+    static_assert(!SPLIT || F32, "pre-split tiles exist for an f32 cache");
     constexpr int PLANES = F32 ? 2 : 1;         // staged bf16 planes per tile: hi (+ lo for an f32 cache)
     constexpr int KS = HD / 32;                 // k steps of the score MFMA
     constexpr int DT = HD / 16;                 // 16-wide head-dim tiles of the output
@@ -209,6 +286,21 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
         }
     };
 
+    // SPLIT: wave w copies plane w of a pre-split tile (K hi, K lo, V^T hi, V^T lo) into LDS buffer buf; the
+    // caller waits for its DMAs before the barrier that publishes the buffer
+    auto copy = [&](int tile, int buf) {
+        if constexpr (SPLIT) {
+            using T = SplitTile<HD>;
+            static_assert(T::KSTRIDE == KSTRIDE && T::VSTRIDE == VSTRIDE, "one layout");
+            const char* src = static_cast<const char*>(p.kv_split) +
+                              (static_cast<int64_t>(blockIdx.y) * p.kv_split_tiles + tile) * T::BYTES +
+                              (wave < 2 ? wave * T::KPLANE : 2 * T::KPLANE + (wave - 2) * T::VPLANE);
+            const uint32_t lds = lds_offset(wave < 2 ? &ks[wave][buf][0] : &vt[wave - 2][buf][0]);
+            const int blocks = (wave < 2 ? T::KPLANE : T::VPLANE) / 1024;
+            for (int i = 0; i < blocks; ++i) dma16(src + 1024 * i, 16 * lane, lds + 1024 * i);
+        }
+    };
+
     // o: the output accumulators; l: the running row sums, taken by the matrix cores as a ones row of V^T times
     // P^T (every entry of l[qt] holds the sum of the lane's query row, so no cross-lane step is needed)
     f32x4 o[2][DT], l[2];
@@ -225,7 +317,10 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
     auto step = [&](int tile, auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
         const int buf = tile & 1;
-        if (tile + 1 < tiles) load(tile + 1);
+        if (tile + 1 < tiles) {
+            if constexpr (SPLIT) copy(tile + 1, buf ^ 1);
+            else load(tile + 1);
+        }
 
         // scores: s[i][qt] = S[keys 64 tile + 16 i + 4 q + j][query row (qt, lane % 16)]
         // the K fragments are read ahead so that the reads overlap: the whole tile at head dim 64, one 16-key
@@ -330,11 +425,19 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
             }
         }
 
-        if (tile + 1 < tiles) stage(tile + 1, buf ^ 1);
+        if (tile + 1 < tiles) {
+            if constexpr (SPLIT) wait_vm<0>();
+            else stage(tile + 1, buf ^ 1);
+        }
         block_barrier();
     };
-    load(0);
-    stage(0, 0);
+    if constexpr (SPLIT) {
+        copy(0, 0);
+        wait_vm<0>();
+    } else {
+        load(0);
+        stage(0, 0);
+    }
     block_barrier();
     for (int tile = 0; tile < min(unmasked, tiles); ++tile) step(tile, std::false_type{});
     for (int tile = unmasked; tile < tiles; ++tile) step(tile, std::true_type{});
@@ -380,18 +483,39 @@ extern "C" int dlk_attention_prefill_eligible(const dlk_attention_params* p) {
            p->splits == 1 && p->ldq % 4 == 0 && p->ldo % 4 == 0;
 }
 
+extern "C" int64_t dlk_attention_split_bytes(const dlk_attention_params* p) {
+    if (p->kv_bf16 || !dlk_attention_prefill_eligible(p)) return 0;
+    const int64_t tiles = (p->capacity + dlk::kKeys - 1) / dlk::kKeys;
+    const int64_t tile = p->hd == 64 ? dlk::SplitTile<64>::BYTES : dlk::SplitTile<128>::BYTES;
+    return static_cast<int64_t>(p->B) * p->KV * tiles * tile;
+}
+
 extern "C" int dlk_attention_prefill(const dlk_attention_params* params, dlh_stream stream_handle) {
     const dlk_attention_params& p = *params;
     if (!dlk_attention_prefill_eligible(&p)) return static_cast<int>(hipErrorInvalidValue);
+    // the pre-split tiles cover every position the cache can hold
+    if (p.kv_split && (p.kv_bf16 || static_cast<int64_t>(p.kv_split_tiles) * dlk::kKeys < p.capacity ||
+                       reinterpret_cast<uintptr_t>(p.kv_split) % 16 != 0))
+        return static_cast<int>(hipErrorInvalidValue);
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
     const int per_head = dlk::kRows / (p.H / p.KV);
     const dim3 grid((p.L + per_head - 1) / per_head, p.B * p.KV);
+    const dim3 threads(dlk::kThreads);
     if (p.kv_bf16) {
-        if (p.hd == 64) hipLaunchKernelGGL((dlk::attention_prefill<uint16_t, 64>), grid, dim3(dlk::kThreads), 0, stream, p);
-        else hipLaunchKernelGGL((dlk::attention_prefill<uint16_t, 128>), grid, dim3(dlk::kThreads), 0, stream, p);
+        if (p.hd == 64) hipLaunchKernelGGL((dlk::attention_prefill<uint16_t, 64, false>), grid, threads, 0, stream, p);
+        else hipLaunchKernelGGL((dlk::attention_prefill<uint16_t, 128, false>), grid, threads, 0, stream, p);
+    } else if (p.kv_split) {
+        const dim3 tiles(p.kv_split_tiles, p.B * p.KV);
+        if (p.hd == 64) {
+            hipLaunchKernelGGL((dlk::split_kv<64>), tiles, threads, 0, stream, p);
+            hipLaunchKernelGGL((dlk::attention_prefill<float, 64, true>), grid, threads, 0, stream, p);
+        } else {
+            hipLaunchKernelGGL((dlk::split_kv<128>), tiles, threads, 0, stream, p);
+            hipLaunchKernelGGL((dlk::attention_prefill<float, 128, true>), grid, threads, 0, stream, p);
+        }
     } else {
-        if (p.hd == 64) hipLaunchKernelGGL((dlk::attention_prefill<float, 64>), grid, dim3(dlk::kThreads), 0, stream, p);
-        else hipLaunchKernelGGL((dlk::attention_prefill<float, 128>), grid, dim3(dlk::kThreads), 0, stream, p);
+        if (p.hd == 64) hipLaunchKernelGGL((dlk::attention_prefill<float, 64, false>), grid, threads, 0, stream, p);
+        else hipLaunchKernelGGL((dlk::attention_prefill<float, 128, false>), grid, threads, 0, stream, p);
     }
     return static_cast<int>(hipGetLastError());
 }

@@ -19,6 +19,31 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// wait until at most n vector-memory operations of this wave are outstanding (lgkm and exp counts untouched)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// 16-byte global->LDS DMA: this lane's 16 bytes at base + offset land at LDS offset lds_base + 16 * lane (base
+// and lds_base wave-uniform).  Issued as inline asm so that the compiler's own wait insertion does not see it
+// (it would drain every DMA in flight before each LDS read): the caller waits for it explicitly (wait_vm) before
+// the work-group barrier that publishes the LDS data.  The compiler's own waits for its loads stay correct (the
+// count of operations issued after a load only grows with the DMAs, so they wait longer, never shorter).
+__device__ __forceinline__ void dma16(const void* base, uint32_t offset, uint32_t lds_base) {
+    // M0 (the LDS destination) is reserved by the compiler: saved and restored around the DMA
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(offset), "s"(base), "s"(lds_base)
+                 : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
 /// f32 -> bf16, round to nearest even, NaN quieted (reference include/dl/half.h:43-47).
 __device__ __forceinline__ uint16_t f32_to_bf16(float v) {
     const uint32_t b = __float_as_uint(v);

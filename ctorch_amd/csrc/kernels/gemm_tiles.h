@@ -109,30 +109,6 @@ inline bool eligible(const dlk_gemv_params& p) {
            reinterpret_cast<uintptr_t>(p.stage) % 16 == 0;
 }
 
-// wait until at most n vector-memory operations of this wave are outstanding (lgkm and exp counts untouched)
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// 16-byte global->LDS DMA: this lane's 16 bytes at base + offset land at LDS offset lds_base + 16 * lane (base
-// and lds_base wave-uniform).  Issued as inline asm so that the compiler's own wait insertion does not see it
-// (it would drain every DMA in flight before each LDS read); the ring's waits are explicit (wait_vm) and no
-// other vector-memory operation is issued inside the ring loop.
-__device__ __forceinline__ void dma16(const void* base, uint32_t offset, uint32_t lds_base) {
-    // M0 (the LDS destination) is reserved by the compiler: saved and restored around the DMA
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "v"(offset), "s"(base), "s"(lds_base)
-                 : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
-}
-
 // Work-group barrier for the DMA ring: the caller has waited for its own DMA; no fence (a fence over LDS would
 // wait for every DMA in flight).  The empty asm keeps the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void ring_barrier() {

@@ -141,7 +141,7 @@ typedef struct dlk_attention_params {
     /* One position on the matrix-core kernel: the QKV projection's key-split partials, left unreduced by it
        (dlk_gemv_params.defer_reduce).  The attention sums them in slice order for its sequence's q, k and v
        columns, applies the RMSNorm factor (row sums of squares after the dots) and RoPE at *position, and writes
-       the new K/V row into the cache at *position before reading the keys.  Layout: [qkv_splits][B][qkv_width]
+       the new K/V row into the cache at *position (and uses the finished row for that key in place of the cache's).  Layout: [qkv_splits][B][qkv_width]
        dot products (q columns, then k, then v), then [qkv_splits][B] sums of squares. */
     const float* qkv_partial;
     int qkv_splits, qkv_width, qkv_K, qkv_norm;
@@ -151,6 +151,11 @@ typedef struct dlk_attention_params {
     void* stage_out;         /* prefill kernel only: write the output rows (row b * L + l, K = H * hd) split into
                                 bf16 hi + lo in the staging layout of the tiled projection that reads them, instead
                                 of out (see dlk_gemv_params.stage_out) */
+    void* kv_split;          /* prefill kernel over an f32 cache: dlk_attention_split_bytes of workspace
+                                (kv_split_tiles 64-key tiles per (b, kv head), covering the capacity).  A preparation
+                                launch splits the live K/V tiles into bf16 hi + lo planes once, and the attention
+                                copies them into LDS as they are instead of splitting each tile it reads */
+    int kv_split_tiles;
 } dlk_attention_params;
 
 /* Keys per split of a short one-position decode over a bf16 cache (few keys in all): 256 or 512, one work-group. */
@@ -176,6 +181,9 @@ int dlk_attention_prefill_eligible(const dlk_attention_params* p);
 int dlk_attention_matrix_eligible(const dlk_attention_params* p);
 int dlk_attention_matrix_decode(const dlk_attention_params* p, dlh_stream stream);
 int dlk_attention_prefill(const dlk_attention_params* p, dlh_stream stream);
+/* Bytes of kv_split workspace for these parameters: the capacity's 64-key tiles of every (b, kv head) as bf16
+   hi + lo planes of K and V^T (0: no such path, a bf16 cache or not the prefill kernel). */
+int64_t dlk_attention_split_bytes(const dlk_attention_params* p);
 
 /* ------------------------------------------------------------------------------------------------------
  * Small kernels of the token loop and the tensor API.

@@ -257,6 +257,15 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         // the label names what the launch leaves: finished rows, or the partials the attention finishes
         issue(observer, qkv.defer_reduce ? "qkv_split" : "qkv_rope_append", qkv_bytes,
               [p = qkv, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "QKV projection"); });
+        // Prefill over an f32 cache: the K/V tiles are split into bf16 planes once for the launch (a workspace
+        // covering the capacity; kept within 1 GiB, past which the kernel splits each tile it reads itself)
+        const int64_t split_bytes = length > 1 ? dlk_attention_split_bytes(&a) : 0;
+        if (split_bytes > 0 && split_bytes <= (int64_t(1) << 30)) {
+            if (!ws.kv_split.defined() || ws.kv_split.numel() * 4 < split_bytes || !(ws.kv_split.device() == device))
+                ws.kv_split = empty_tensor({(split_bytes + 3) / 4}, DType::f32, device);
+            a.kv_split = mutable_data(ws.kv_split);
+            a.kv_split_tiles = static_cast<int>((cache.capacity() + 63) / 64);
+        }
         const double bytes = 2.0 * kv_bytes_per * static_cast<double>(cache.length() + length);
         issue(observer, "attention", bytes,
               [a, &context](bool) { hip_check(dlk_attention(&a, context.stream), "attention"); });

@@ -20,6 +20,7 @@ struct DecodeWorkspace {
     Tensor stage_ffn; ///< prefill: the SwiGLU rows already split for the down projection's tiled path
     Tensor stage_attn; ///< prefill: the attention rows already split for the output projection's tiled path
     Tensor stage; ///< prefill projections: activation rows split into bf16 hi + lo, per-row norm factors
+    Tensor kv_split; ///< prefill attention over an f32 cache: the K/V tiles split into bf16 hi + lo planes
     /// Points `p` at the staging workspace when its shape takes the tiled prefill path and at the split
     /// workspace when its launch would split the keys (both grown as needed).
     void attach_workspace(dlk_gemv_params& p, Device device);
