@@ -90,7 +90,7 @@ __device__ __forceinline__ void split4(const u32x4 w, u32x2& hi, u32x2& lo) {
 // would repeat on each tile it reads (C5: 128 work-groups per pair), and the attention copies a tile into LDS
 // with the global->LDS DMA, no registers or vector-ALU work on the way.
 template <int HD> struct SplitTile {
-    static constexpr int KSTRIDE = HD + 8, VSTRIDE = kKeys + 8;
+    static constexpr int KSTRIDE = HD + 16, VSTRIDE = kKeys + 8;
     static constexpr int KPLANE = kKeys * KSTRIDE * 2, VPLANE = HD * VSTRIDE * 2; // bytes
     static constexpr int BYTES = 2 * KPLANE + 2 * VPLANE;
     static_assert(KPLANE % 1024 == 0 && VPLANE % 1024 == 0, "whole 1 KB DMA blocks");
@@ -166,7 +166,9 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
     constexpr int PLANES = F32 ? 2 : 1;         // staged bf16 planes per tile: hi (+ lo for an f32 cache)
     constexpr int KS = HD / 32;                 // k steps of the score MFMA
     constexpr int DT = HD / 16;                 // 16-wide head-dim tiles of the output
-    constexpr int KSTRIDE = HD + 8;             // bf16 per staged K row
+    // bf16 per staged K row: 160 (288) bytes at head dim 64 (128), where the 16-byte fragment reads of 16 rows
+    // hit no LDS bank twice (measured on MI355X: a 144- or 272-byte row costs ~4 conflict cycles per read)
+    constexpr int KSTRIDE = HD + 16;
     constexpr int VSTRIDE = kKeys + 8;          // bf16 per staged V^T row (one head-dim column)
     constexpr int DPP = 16 / sizeof(KT);        // head-dim values per 16-byte piece
     constexpr int NG = HD / DPP;                // pieces per K (or V) row
