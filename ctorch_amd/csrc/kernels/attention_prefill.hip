@@ -360,8 +360,7 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
 
         // online softmax per query row (the lane's column; lanes l, l^16, l^32, l^48 share it), in base 2
         bf16x8 ph[2][2], pl[2][2]; // [key block u: tiles 2u, 2u+1][qt]
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        auto softmax = [&](int qt) {
             float mx = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -383,7 +382,10 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
 #pragma unroll
                 for (int j = 0; j < 4; ++j) s[i][qt][j] = __builtin_amdgcn_exp2f(s[i][qt][j] - m_new);
             m_run[qt] = m_new;
-            if (!__all(alpha == 1.0f)) { // the running maxima of the wave's rows moved
+            // f32 cache: unconditional (alpha = 1 when the maxima stayed), since a branch would split the tile into
+            // basic blocks and the scheduler could not put this work under the MFMAs; the bf16 kernels keep the
+            // branch, whose registers hold at head dim 128 only with it
+            if (F32 || !__all(alpha == 1.0f)) {
                 l[qt] *= alpha;
 #pragma unroll
                 for (int d = 0; d < DT; ++d) o[qt][d] *= alpha;
@@ -393,8 +395,9 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
                 split8_pairs(f32x8{s[2 * u][qt][0], s[2 * u][qt][1], s[2 * u][qt][2], s[2 * u][qt][3],
                              s[2 * u + 1][qt][0], s[2 * u + 1][qt][1], s[2 * u + 1][qt][2], s[2 * u + 1][qt][3]},
                        ph[u][qt], pl[u][qt]);
-        }
-
+        };
+        softmax(0);
+        softmax(1);
         // O^T += V^T P^T: lane (d = 16 dt + lane % 16, q) supplies V[keys 32 u + 4 q .. +4, 32 u + 16 + 4 q .. +4][d]
 #pragma unroll
         for (int u = 0; u < 2; ++u)
