@@ -90,8 +90,11 @@ __device__ __forceinline__ void split4(const u32x4 w, u32x2& hi, u32x2& lo) {
 // would repeat on each tile it reads (C5: 128 work-groups per pair), and the attention copies a tile into LDS
 // with the global->LDS DMA, no registers or vector-ALU work on the way.
 template <int HD> struct SplitTile {
-    static constexpr int KSTRIDE = HD + 16, VSTRIDE = kKeys + 8;
-    static constexpr int KPLANE = kKeys * KSTRIDE * 2, VPLANE = HD * VSTRIDE * 2; // bytes
+    // V^T rows of 136 bytes: the paired 8-byte fragment reads (ds_read2_b64, 32 bytes apart) of 16 rows hit no
+    // LDS bank twice (measured on MI355X: 144-byte rows cost ~8 conflict cycles per read); each plane is padded
+    // to whole 1 KB DMA blocks
+    static constexpr int KSTRIDE = HD + 16, VSTRIDE = kKeys + 4;
+    static constexpr int KPLANE = kKeys * KSTRIDE * 2, VPLANE = (HD * VSTRIDE * 2 + 1023) / 1024 * 1024; // bytes
     static constexpr int BYTES = 2 * KPLANE + 2 * VPLANE;
     static_assert(KPLANE % 1024 == 0 && VPLANE % 1024 == 0, "whole 1 KB DMA blocks");
 };
@@ -169,13 +172,16 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
     // bf16 per staged K row: 160 (288) bytes at head dim 64 (128), where the 16-byte fragment reads of 16 rows
     // hit no LDS bank twice (measured on MI355X: a 144- or 272-byte row costs ~4 conflict cycles per read)
     constexpr int KSTRIDE = HD + 16;
-    constexpr int VSTRIDE = kKeys + 8;          // bf16 per staged V^T row (one head-dim column)
+    // bf16 per staged V^T row (one head-dim column): the pre-split tile's conflict-free 68, or 72, where the
+    // 4-byte transposing stores of the in-kernel staging spread over the banks
+    constexpr int VSTRIDE = SPLIT ? SplitTile<HD>::VSTRIDE : kKeys + 8;
+    constexpr int VELEMS = SPLIT ? SplitTile<HD>::VPLANE / 2 : HD * VSTRIDE; // bf16 per V^T plane
     constexpr int DPP = 16 / sizeof(KT);        // head-dim values per 16-byte piece
     constexpr int NG = HD / DPP;                // pieces per K (or V) row
     constexpr int LOADS = kKeys * NG / kThreads; // K pieces per thread per tile (and V pieces, in key pairs)
     static_assert(kKeys * NG % kThreads == 0 && LOADS % 2 == 0, "whole loads; V pieces come in key pairs");
     __shared__ __attribute__((aligned(16))) uint16_t ks[PLANES][2][kKeys * KSTRIDE];
-    __shared__ __attribute__((aligned(16))) uint16_t vt[PLANES][2][HD * VSTRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[PLANES][2][VELEMS];
 
     const int t = threadIdx.x, lane = t % kWave, q = lane / 16;
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
