@@ -71,7 +71,7 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <typename KT, int HD, int W>
+template <typename KT, int HD, int W, bool FINISH>
 __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attention_params p) {
     constexpr bool F32 = sizeof(KT) == 4;
     constexpr int PLANES = F32 ? 2 : 1;      // bf16 planes of the staged V^T: hi (+ lo for an f32 cache)
@@ -105,13 +105,9 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
         }
         return;
     }
-    // the split's live keys in equal runs of whole tiles per wave (a split past most of the sequence's keys, or
-    // a chunk sized for a longer sequence, keeps every wave busy for fewer tiles)
-    const int64_t s_begin = static_cast<int64_t>(split) * p.chunk;
-    const int64_t k_end = min(S, s_begin + p.chunk);
-    const int live = static_cast<int>(k_end - s_begin);
-    const int per_wave = ((live + W - 1) / W + kTileKeys - 1) / kTileKeys * kTileKeys;
-    const int64_t w_begin = s_begin + static_cast<int64_t>(wave) * per_wave;
+    const int per_wave = p.chunk / W;
+    const int64_t k_end = min(S, static_cast<int64_t>(split) * p.chunk + p.chunk);
+    const int64_t w_begin = static_cast<int64_t>(split) * p.chunk + static_cast<int64_t>(wave) * per_wave;
     const int keys = static_cast<int>(max<int64_t>(0, min<int64_t>(k_end, w_begin + per_wave) - w_begin));
     const int tiles = (keys + kTileKeys - 1) / kTileKeys;
 
@@ -262,18 +258,27 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
     // part of o_s (free until the merge).  The one wave whose keys hold the new position (in the last active
     // split's work-group) also finishes the new K/V row: it writes the row into the cache for later steps and
     // puts it in place of what its tile load returned for that key, so no wave waits on the write.
-    const bool finish = p.qkv_partial != nullptr;
+    constexpr bool finish = FINISH; // the launch chooses FINISH = (qkv_partial != NULL)
     const int64_t newest = S - 1;
     const bool holder = finish && split == active - 1 && newest >= w_begin && newest < w_begin + keys;
     const int patch_tile = holder ? static_cast<int>(newest - w_begin) / kTileKeys : -1;
     const int patch_key = holder ? static_cast<int>(newest - w_begin) % kTileKeys : 0;
     Tile a, c;
-    if (tiles > 0) load(0, a);
     {
         const float qs = p.scale * 1.4426950408889634f;
         const float z = col < G ? qs : 0.0f;
-        const float* qrow;
-        if (finish) {
+        // q rows finished here, from LDS: a path of their own, so that the reads are typed (a pointer that may
+        // hold LDS or global addresses would take flat loads)
+        auto split_q = [&](const float* qrow) {
+#pragma unroll
+            for (int st = 0; st < KS; ++st) {
+                const float4 x0 = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q);
+                const float4 x1 = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q + 4);
+                split8(f32x8{x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w} * z, qh[st], ql[st]);
+            }
+        };
+        if constexpr (finish) {
+            if (tiles > 0) load(0, a);
             constexpr int kBatch = 8; // slices requested at once
             constexpr int UNITS = HD / 4; // 4-dim units per head row
             const int width = p.qkv_width;
@@ -356,19 +361,27 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
                 }
             }
             // the staged rows are read back by the lanes of this wave only (LDS operations of a wave complete in
-            // order); the barrier keeps the compiler from moving the reads above the writes
+            // order); the barriers keep the compiler from moving the reads above the writes, and the merge's
+            // writes of o_s above the reads
             __asm__ volatile("" ::: "memory");
-            qrow = stage + min(col, G - 1) * HD;
+            split_q(stage + min(col, G - 1) * HD);
+            __asm__ volatile("" ::: "memory");
         } else {
-            qrow = p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G + min(col, G - 1)) * HD;
-        }
+            // the query loads first, then the first tile's, then the split (which waits for the query rows only)
+            const float* qrow =
+                p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G + min(col, G - 1)) * HD;
+            float4 x[KS][2];
 #pragma unroll
-        for (int st = 0; st < KS; ++st) {
-            const float4 x0 = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q);
-            const float4 x1 = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q + 4);
-            split8(f32x8{x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w} * z, qh[st], ql[st]);
+            for (int st = 0; st < KS; ++st) {
+                x[st][0] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q);
+                x[st][1] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q + 4);
+            }
+            if (tiles > 0) load(0, a);
+#pragma unroll
+            for (int st = 0; st < KS; ++st)
+                split8(f32x8{x[st][0].x, x[st][0].y, x[st][0].z, x[st][0].w, x[st][1].x, x[st][1].y, x[st][1].z,
+                             x[st][1].w} * z, qh[st], ql[st]);
         }
-        __asm__ volatile("" ::: "memory");
     }
     // The holder's new key in its tile's registers (K: lanes col = key % 16 of half key / 16 hold dims
     // 32 st + 8 q ..; V: lanes col = key / 2, member key % 2 hold pieces q + 4 i), in the cache's type.
@@ -385,7 +398,7 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
         }
     };
     auto patch = [&](int tile, Tile& dst) {
-        if (tile != patch_tile) return;
+        if (!FINISH || tile != patch_tile) return;
         __asm__ volatile("" ::: "memory"); // the row is read here, not kept in registers through the loop
         const int u = patch_key / 16, kc = patch_key % 16, vc = patch_key / 2, ve = patch_key % 2;
 #pragma unroll
@@ -471,11 +484,13 @@ int launch(const dlk_attention_params& p, hipStream_t stream) {
     // eight)
     if constexpr (HD == 64) {
         if (p.chunk <= 512 && p.splits == 1) {
-            hipLaunchKernelGGL((attention_matrix<KT, HD, 8>), grid, dim3(8 * kWave), 0, stream, p);
+            if (p.qkv_partial) hipLaunchKernelGGL((attention_matrix<KT, HD, 8, true>), grid, dim3(8 * kWave), 0, stream, p);
+            else hipLaunchKernelGGL((attention_matrix<KT, HD, 8, false>), grid, dim3(8 * kWave), 0, stream, p);
             return static_cast<int>(hipGetLastError());
         }
     }
-    hipLaunchKernelGGL((attention_matrix<KT, HD, 4>), grid, dim3(4 * kWave), 0, stream, p);
+    if (p.qkv_partial) hipLaunchKernelGGL((attention_matrix<KT, HD, 4, true>), grid, dim3(4 * kWave), 0, stream, p);
+    else hipLaunchKernelGGL((attention_matrix<KT, HD, 4, false>), grid, dim3(4 * kWave), 0, stream, p);
     return static_cast<int>(hipGetLastError());
 }
 
