@@ -129,6 +129,12 @@ int dlh_event_elapsed(dlh_event start, dlh_event stop, float* milliseconds) {
 int dlh_capture_begin(dlh_stream stream) {
     return code(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal));
 }
+int dlh_stream_capturing(dlh_stream stream, int* capturing) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(as_stream(stream), &status);
+    *capturing = status == hipStreamCaptureStatusActive ? 1 : 0;
+    return code(e);
+}
 int dlh_capture_end(dlh_stream stream, dlh_graph* executable) {
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(as_stream(stream), &graph);

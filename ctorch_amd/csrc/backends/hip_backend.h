@@ -63,6 +63,8 @@ int dlh_event_elapsed(dlh_event start, dlh_event stop, float* milliseconds);
 
 /* Stream capture into an executable graph (thread-local capture mode). */
 int dlh_capture_begin(dlh_stream stream);
+/* *capturing = 1 while the stream records into a graph. */
+int dlh_stream_capturing(dlh_stream stream, int* capturing);
 int dlh_capture_end(dlh_stream stream, dlh_graph* executable);
 int dlh_graph_launch(dlh_graph executable, dlh_stream stream);
 int dlh_graph_destroy(dlh_graph executable);

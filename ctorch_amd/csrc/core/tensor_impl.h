@@ -45,5 +45,10 @@ void copy_into(const Tensor& target, const Tensor& source);
 /// Makes `tensor` refer to `value`'s storage and layout in place (identity kept for all handles).
 void rebind(const Tensor& tensor, const Tensor& value);
 std::string shape_string(const Shape& shape);
+/// A counter that module weight loads and device moves advance (Module::load_state_dict, Module::to): caches
+/// derived from parameter values (the repacked projection weights of the batched decode) are valid while it
+/// stays where it was when they were built.  Writes through a raw data pointer do not advance it.
+uint64_t parameter_epoch();
+void advance_parameter_epoch();
 
 } // namespace dl::detail

@@ -184,6 +184,45 @@ int launch_waves(const dlk_gemv_params& p) {
 
 } // namespace
 
+namespace {
+
+// One thread per 16-byte piece of the output: piece (tile t, k step s, lane l) = row l % 16 of tile t, columns
+// 32 s + 8 (l / 16) .. +8.
+__global__ __launch_bounds__(256) void pack_tiles(const uint16_t* w0, const uint16_t* w1, int swiglu, int64_t tiles,
+                                                  int64_t K, uint16_t* out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t steps = K / 32;
+    if (i >= tiles * steps * dlk::kWave) return;
+    const int lane = static_cast<int>(i % dlk::kWave);
+    const int64_t block = i / dlk::kWave, t = block / steps, s = block % steps;
+    const int r = lane % 16, q = lane / 16;
+    const uint16_t* row = swiglu ? (r & 1 ? w1 : w0) + (8 * t + r / 2) * K : w0 + (16 * t + r) * K;
+    *reinterpret_cast<uint4*>(out + block * 512 + 8 * lane) = *reinterpret_cast<const uint4*>(row + 32 * s + 8 * q);
+}
+
+} // namespace
+
+extern "C" int dlk_pack_tiles(const void* w0, const void* w1, int swiglu, int64_t rows, int64_t K, void* out,
+                              dlh_stream stream) {
+    const int64_t per_tile = swiglu ? 8 : 16;
+    if (!w0 || !out || (swiglu && !w1) || rows <= 0 || K <= 0 || K % 32 != 0 || rows % per_tile != 0)
+        return static_cast<int>(hipErrorInvalidValue);
+    const int64_t pieces = rows / per_tile * (K / 32) * dlk::kWave;
+    const int64_t blocks = (pieces + 255) / 256;
+    if (blocks > INT32_MAX) return static_cast<int>(hipErrorInvalidValue);
+    hipLaunchKernelGGL(pack_tiles, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w0),
+                       static_cast<const uint16_t*>(w1), swiglu, rows / per_tile, K, static_cast<uint16_t*>(out));
+    return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int dlk_gemv_uses_rows(const dlk_gemv_params* p) {
+    if (dlk::tiles::eligible(*p) || !dlk::gemm::eligible(*p)) return 0;
+    dlk_gemv_params first = *p; // the first launch of kMaxRows rows decides between the wide and the rows kernel
+    first.M = std::min(p->M, dlk::gemm::kMaxRows);
+    return dlk::gemm::wide_eligible(first) ? 0 : 1;
+}
+
 extern "C" int64_t dlk_gemv_split_floats(const dlk_gemv_params* p) {
     if (dlk::tiles::eligible(*p)) return 0;
     if (!dlk::gemm::eligible(*p)) return 0;

@@ -42,6 +42,8 @@ typedef struct dlk_gemv_params {
     int M, K;
     int nseg;               /* 1..3 weight segments stacked along n (STORE: their outputs side by side in y) */
     const void* w[3];       /* [seg_rows[i], K] row-major */
+    const void* w_tiles[3]; /* optional, bf16: segment i repacked by dlk_pack_tiles, which the batched matrix-core
+                               path reads instead of w (1 KB contiguous per load instruction) */
     int seg_rows[3];
     int w_bf16;
     int apply_norm;         /* fuse the preceding RMSNorm: scale row m by 1/sqrt(mean(x^2)+eps), weight g */
@@ -98,6 +100,14 @@ typedef struct dlk_gemv_params {
                                of y; that launch then takes it as its stage with stage_ready set */
 } dlk_gemv_params;
 
+/* Repacks bf16 weights for the batched matrix-core path: for each 16-row tile and 32-wide k step a 1 KB block
+   whose 16 bytes at 16 l hold tile row l % 16, columns 32 s + 8 (l / 16) .. +8 (the MFMA operand of lane l).
+   swiglu = 0: rows of w0 [rows, K], tile t = rows 16 t .. +16.  swiglu = 1: w0 = gate, w1 = up, each [rows, K];
+   tile t interleaves gate and up rows 8 t .. +8 (tile row 2 j: gate 8 t + j, 2 j + 1: up 8 t + j).  out holds
+   rows * K (swiglu: 2 * rows * K) bf16. */
+int dlk_pack_tiles(const void* w0, const void* w1, int swiglu, int64_t rows, int64_t K, void* out, dlh_stream stream);
+/* 1 when dlk_gemv takes the batched matrix-core kernel (gemm_rows, the one that reads w_tiles) for this launch. */
+int dlk_gemv_uses_rows(const dlk_gemv_params* p);
 /* Floats of workspace that lets dlk_gemv split the keys of this launch (0 when it would not split). */
 int64_t dlk_gemv_split_floats(const dlk_gemv_params* p);
 /* Key slices dlk_gemv will use for this launch as attached (1: no split). */

@@ -55,6 +55,30 @@ void DecodeWorkspace::attach_workspace(dlk_gemv_params& p, Device device) {
     p.split_capacity = split.numel();
 }
 
+const void* DecodeWorkspace::tiles_of(const Tensor& w0, const Tensor* w1, dlh_stream stream) {
+    if (!pack_weights || w0.dtype() != DType::bf16 || w0.ndim() != 2 || !w0.is_contiguous()) return nullptr;
+    const Index rows = w0.size(0), K = w0.size(1);
+    if (w1 && (w1->dtype() != DType::bf16 || w1->shape() != w0.shape() || !w1->is_contiguous())) return nullptr;
+    if (K % 32 != 0 || rows % (w1 ? 8 : 16) != 0) return nullptr;
+    int capturing = 0;
+    hip_check(dlh_stream_capturing(stream, &capturing), "stream capture status");
+    const uint64_t epoch = parameter_epoch();
+    if (epoch != packed_epoch_) {
+        if (capturing) return nullptr;
+        packed_.clear();
+        packed_epoch_ = epoch;
+    }
+    const void* key = w0.data<void>();
+    const auto it = packed_.find(key);
+    if (it != packed_.end() && it->second.source.data<void>() == key) return it->second.tiles.data<void>();
+    if (capturing) return nullptr;
+    Tensor tiles = empty_tensor({(w1 ? 2 : 1) * rows * K}, DType::bf16, w0.device());
+    hip_check(dlk_pack_tiles(key, w1 ? w1->data<void>() : nullptr, w1 ? 1 : 0, rows, K, mutable_data(tiles), stream),
+              "weight repack");
+    packed_[key] = Packed{w0, tiles};
+    return tiles.data<void>();
+}
+
 namespace {
 const void* norm_data(const nn::RMSNorm& norm, int& bf16) {
     const auto& w = norm.weight();
@@ -197,6 +221,12 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
     // attention may read its partials), which already fits both launches
     ws.attach_workspace(qkv, device);
     share_stage(qkv);
+    if (dlk_gemv_uses_rows(&qkv)) {
+        qkv.w_tiles[0] = ws.tiles_of(attention.query().weight(), nullptr, context.stream);
+        qkv.w_tiles[1] = ws.tiles_of(attention.key().weight(), nullptr, context.stream);
+        qkv.w_tiles[2] = ws.tiles_of(attention.value().weight(), nullptr, context.stream);
+    }
+    if (dlk_gemv_uses_rows(&out)) out.w_tiles[0] = ws.tiles_of(attention.output().weight(), nullptr, context.stream);
 
     // 3. split-K attention over the cache (reads the device length, sees the keys just appended)
     {
@@ -324,6 +354,8 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
             down.stage_bytes = ws.stage_ffn.numel() * 4;
             down.stage_ready = 1;
         }
+        if (dlk_gemv_uses_rows(&p)) p.w_tiles[0] = ws.tiles_of(ff.gate().weight(), &ff.up().weight(), context.stream);
+        if (dlk_gemv_uses_rows(&down)) down.w_tiles[0] = ws.tiles_of(ff.down().weight(), nullptr, context.stream);
         issue(observer, "gate_up_silu", static_cast<double>(2 * F * d) * (gb ? 2 : 4),
               [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "gate/up projection"); });
     }

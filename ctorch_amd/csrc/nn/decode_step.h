@@ -6,7 +6,9 @@
 
 #include "nn/ops_internal.h"
 
+#include <cstdint>
 #include <functional>
+#include <unordered_map>
 #include <utility>
 
 namespace dl::detail {
@@ -26,6 +28,22 @@ struct DecodeWorkspace {
     void attach_workspace(dlk_gemv_params& p, Device device);
     void ensure(const nn::TransformerDecoderLayer& layer, Index rows, Index heads_total, Index hidden_features,
                 int splits, Device device);
+
+    /// Batched decode: bf16 projection weights repacked in the matrix-core kernel's tile order (dlk_pack_tiles),
+    /// so that each of its weight loads reads 1 KB contiguous.  Off unless set (it costs a second copy of every
+    /// packed weight in HBM); a weight is packed on the first eager launch that takes that kernel, and the packs
+    /// are dropped when the parameter epoch moves (weights loaded or moved).
+    bool pack_weights = false;
+    /// The packed tiles of `w0` [rows, K] (with `w1`: gate and up, interleaved for the SwiGLU launch), or null
+    /// (packing off, not bf16, a shape the pack does not cover, or no current pack while `stream` captures).
+    const void* tiles_of(const Tensor& w0, const Tensor* w1, dlh_stream stream);
+
+private:
+    struct Packed {
+        Tensor source, tiles; // source keeps the weight's storage (the key) alive while the pack exists
+    };
+    std::unordered_map<const void*, Packed> packed_;
+    uint64_t packed_epoch_ = 0;
 };
 
 /// Launch hook for profiling (null in normal operation).  Every launch of a step is handed over as a closure

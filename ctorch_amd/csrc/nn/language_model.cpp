@@ -23,6 +23,10 @@ DecoderLM::DecoderLM(std::shared_ptr<nn::Embedding> embedding, std::shared_ptr<n
         throw std::invalid_argument("embedding / head width differs from the decoder width");
     if (head_->bias()) throw std::invalid_argument("the fused LM head takes a bias-free Linear");
     context_ = &gpu_context(device.index);
+    // the token loop runs many steps over the same weights: the batched decode reads them repacked in its
+    // matrix-core kernel's tile order, a second copy of the bf16 projection and head weights in HBM (1B: 1.6 GB,
+    // 8B: 14 GB) for a faster step (MI355X, 1B at batch 32: 1.44 -> 1.33 ms; 8B at batch 8: 10.2 -> 9.6 ms)
+    ws_.pack_weights = true;
 }
 
 DecoderLM::~DecoderLM() { release_graph(); }
@@ -120,6 +124,7 @@ void DecoderLM::forward_chunk(const Index* ids, Index batch, Index length, std::
         p.partial = static_cast<dlk_sample_partial*>(mutable_data(partial_));
         p.partial_blocks = blocks;
     }
+    if (dlk_gemv_uses_rows(&p)) p.w_tiles[0] = ws_.tiles_of(head_->weight(), nullptr, context->stream);
     issue(observer, "lm_head", static_cast<double>(V * d) * (hb ? 2 : 4),
           [p, context](bool) { hip_check(dlk_gemv(&p, context->stream), "LM head"); });
     if (sample_mode > 0) {

@@ -5,9 +5,18 @@
 #include "dl/nn.h"
 
 #include <algorithm>
+#include <atomic>
 #include <stdexcept>
 #include <unordered_map>
 #include <unordered_set>
+
+namespace dl::detail {
+namespace {
+std::atomic<uint64_t> g_parameter_epoch{1};
+}
+uint64_t parameter_epoch() { return g_parameter_epoch.load(std::memory_order_acquire); }
+void advance_parameter_epoch() { g_parameter_epoch.fetch_add(1, std::memory_order_acq_rel); }
+} // namespace dl::detail
 
 namespace dl::nn {
 
@@ -108,6 +117,7 @@ void Module::load_state_dict(std::span<const NamedTensor> state) {
         const Tensor& target = destination[i].second;
         detail::copy_into(target, values[i].to(target.device()));
     }
+    detail::advance_parameter_epoch();
 }
 
 void Module::to(Device device) {
@@ -117,6 +127,7 @@ void Module::to(Device device) {
         if (tensor.device() == device) continue;
         detail::rebind(tensor, tensor.to(device));
     }
+    detail::advance_parameter_epoch();
 }
 
 } // namespace dl::nn

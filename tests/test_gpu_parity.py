@@ -253,6 +253,36 @@ def test_batched_decode_on_matrix_cores():
     assert np.array_equal(oracle.sample(l1, 1.0, oracle.fold_in((3, 4), 9)), t1[:, -1])
 
 
+def test_batched_decode_reads_weights_loaded_after_its_repacked_copies_were_built():
+    say("case: B=4 bf16 decode (repacked projection weights), then new decoder weights loaded, decode again")
+    cfg = oracle.ModelConfig(vocab=1000, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=1024, context=32,
+                             dtype="bf16")
+    first = oracle.synthesize_weights(cfg, (51, 0), 0.05)
+    ref, gpu = build_pair(cfg, weights=first)
+    B = 4
+    prompt = oracle.random_ids((52, 0), B * 3, cfg.vocab).reshape(B, 3)
+
+    def decode(ref_model):
+        rc, gc = ref_model.make_cache(B), gpu.cache()
+        ids = prompt
+        for step in range(4):  # the prompt, then single-position steps (the batched matrix-core route)
+            want = ref_model.logits(ids, rc)[:, -1]
+            got = gpu.logits(ids, gc)
+            assert np.max(np.abs(got - want)) <= 2e-2, step
+            ids = want.argmax(-1).reshape(B, 1)
+
+    decode(ref)
+    # the decoder's weights change in place; the embedding and the head stay
+    second = oracle.synthesize_weights(cfg, (53, 0), 0.05)
+    merged = {n: (second[n] if n.startswith("decoder.") else v) for n, v in first.items()}
+    state = {n[len("decoder."):]: v for n, v in merged.items() if n.startswith("decoder.")}
+    dtypes = {n: (ct.BF16 if v.dtype == np.uint16 else None) for n, v in state.items()}
+    for name, tensor in gpu.decoder.state().items():
+        state.setdefault(name, tensor)
+    gpu.decoder.load_state(state, dtypes)
+    decode(oracle.OracleLM(cfg, merged, kv_bf16=False))
+
+
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
 def test_head_dim_128_batched_decode_over_a_long_prefix(kv):
     say(f"case: B=8 decode, head dim 128, RoPE base 500000, 1000-token seeded {kv} prefix (the C4 route, small)")
