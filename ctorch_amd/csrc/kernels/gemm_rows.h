@@ -289,7 +289,7 @@ __device__ __forceinline__ void lane_epilogue(const dlk_gemv_params& p, const Ti
 }
 
 template <int EPI, bool NORM, int MT, int NC>
-__global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
+__global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params launch) {
     constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
     constexpr int RM = 16 * MT;            // staged activation rows
     constexpr int KC = chunk_k(MT);        // k per chunk
@@ -306,9 +306,21 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params p) {
     __shared__ double pool_score[kWaves][RM];
     __shared__ int64_t pool_index[kWaves][RM];
 
+    // A SwiGLU launch over more rows than one work-group's tiles may be split over the rows instead of the keys
+    // (row_parts: part y takes rows RM y .. +RM with all of K; no partials, no reduce launch), as the host
+    // splits a launch into 64-row chunks
+    dlk_gemv_params p = launch;
+    const bool by_rows = SWIGLU && launch.row_parts > 1;
+    if (by_rows) {
+        const int m0 = static_cast<int>(blockIdx.y) * RM;
+        p.M = min(RM, launch.M - m0);
+        p.x = launch.x + static_cast<int64_t>(m0) * launch.ldx;
+        p.y = launch.y + static_cast<int64_t>(m0) * launch.ldy;
+        p.m_base = launch.m_base + m0;
+    }
     const int t = threadIdx.x, lane = t % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
-    const int K = p.K, splits = gridDim.y, slice = K / splits, k_begin = blockIdx.y * slice;
+    const int K = p.K, splits = by_rows ? 1 : gridDim.y, slice = K / splits, k_begin = by_rows ? 0 : blockIdx.y * slice;
     const int nchunks = slice / KC;
     const int tiles = tiles_of(p);
     const int my_tile = blockIdx.x * kWaves + wave;

@@ -93,6 +93,7 @@ typedef struct dlk_gemv_params {
     void* stage;
     int64_t stage_bytes;
     int stage_ready;        /* the workspace already holds this launch's split rows (same x, norm weight, M, K) */
+    int row_parts;          /* set by dlk_gemv for a launch it splits over activation rows (callers leave 0) */
     int defer_reduce;       /* QKV on the key-split matrix-core path: leave the partials for the one-position
                                attention to finish (no reduce launch); see dlk_attention_params.qkv_partial */
     void* stage_out;        /* SWIGLU on the tiled path: write silu(gate) * up, split into bf16 hi + lo, in the
