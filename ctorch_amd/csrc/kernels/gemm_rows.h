@@ -638,9 +638,14 @@ constexpr int kWideWaves = 16;
 constexpr int kWideTiles = 4;
 
 inline bool wide_eligible(const dlk_gemv_params& p) {
-    // a residual projection of up to 128 tiles over at most 16 rows and K <= 2048 too (measured on MI355X, O of
-    // the 1B model at batch 4: 8.8 -> 6.3 us; at 32 rows, or K = 5632, the key-split kernel stays faster)
-    const bool small_residual = p.epilogue == DLK_EPI_RESIDUAL && tiles_of(p) <= 128 && p.M <= 16 && p.K <= 2048;
+    // Also over at most 16 rows and K <= 2048: a residual projection of up to 128 tiles, and a QKV projection of
+    // up to 192 with unmerged LoRA (whose partials the attention cannot finish).  Measured on MI355X, the 1B model
+    // with LoRA at batch 4: O 8.8 -> 6.3 us, QKV 11.7 -> 9.5 us, the step 1.333 -> 1.25 ms; at 32 rows, or
+    // K = 5632, the key-split kernel stays faster.
+    const bool lora = p.lora_up[0] || p.lora_up[2];
+    const bool small_residual = (p.epilogue == DLK_EPI_RESIDUAL ? tiles_of(p) <= 128
+                                 : p.epilogue == DLK_EPI_QKV && lora ? tiles_of(p) <= 192 : false) &&
+                                p.M <= 16 && p.K <= 2048;
     return p.epilogue != DLK_EPI_LOGITS && (tiles_of(p) <= kWideTiles || small_residual) && p.M <= 32 &&
            p.K % (32 * kWideWaves) == 0 &&
            p.ldx % 4 == 0;
