@@ -81,6 +81,20 @@ def test_c3_1b_batch_32_over_a_2048_token_prefix():
     greedy_steps(ref, gpu, rc, gc, ids, 2, "C3")
 
 
+def test_1b_width_batch_20_splits_the_swiglu_launch_into_row_parts_of_16_and_4():
+    say("case: 1B widths, 2 layers, batch 20: gate/up over 88 tile groups in row parts of 16 and 4 rows")
+    cfg = oracle.ModelConfig(vocab=1000, layers=2, dimensions=2048, heads=32, kv_heads=8, hidden=5632, context=16,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(3434, 0))
+    B = 20
+    prompt = oracle.random_ids((3535, 0), B * 5, cfg.vocab).reshape(B, 5)
+    rc, gc = ref.make_cache(B), gpu.cache()
+    want = ref.logits(prompt, rc)[:, -1]
+    got = gpu.logits(prompt, gc)
+    assert np.max(np.abs(got - want)) <= 2e-2
+    greedy_steps(ref, gpu, rc, gc, want.argmax(-1).reshape(B, 1), 3, "batch 20")
+
+
 # ------------------------------------------------------------------------------------------ C4
 C4_WIDTH = dict(vocab=32000, dimensions=4096, heads=32, kv_heads=8, hidden=14336, rope_base=500000.0, dtype="bf16")
 
