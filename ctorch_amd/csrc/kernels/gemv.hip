@@ -99,13 +99,17 @@ int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
         if (params.epilogue != DLK_EPI_QKV) p.y = params.y ? params.y + static_cast<int64_t>(m0) * params.ldy : nullptr;
         if (params.residual) p.residual = params.residual + static_cast<int64_t>(m0) * params.ldres;
         p.bump_position = m0 + kMaxRows >= params.M ? params.bump_position : nullptr;
-        if (wide_eligible(p)) {
+        const bool wide_parts = wide_parts_eligible(p);
+        if (wide_parts || wide_eligible(p)) {
             // few weight tiles: one launch, K split over the waves of each tile's work-group
-            const Kernel wide = resolve_gemm(p, row_tiles(p.M), -1);
+            const int parts = wide_parts ? (p.M + 15) / 16 : 1;
+            p.row_parts = parts;
+            const Kernel wide = resolve_gemm(p, wide_parts ? 1 : row_tiles(p.M), -1);
             if (!wide.fn) return static_cast<int>(hipErrorInvalidValue);
             void* wargs[] = {&p};
-            const hipError_t status =
-                hipLaunchKernel(wide.fn, dim3(tiles_of(p)), dim3(kWideWaves * dlk::kWave), wargs, 0, stream);
+            const hipError_t status = hipLaunchKernel(wide.fn, dim3(tiles_of(p), parts),
+                                                      dim3(kWideWaves * dlk::kWave), wargs, 0, stream);
+            p.row_parts = 0;
             if (status != hipSuccess) return static_cast<int>(status);
             continue;
         }
@@ -237,7 +241,7 @@ extern "C" int dlk_gemv_uses_rows(const dlk_gemv_params* p) {
     if (dlk::tiles::eligible(*p) || !dlk::gemm::eligible(*p)) return 0;
     dlk_gemv_params first = *p; // the first launch of kMaxRows rows decides between the wide and the rows kernel
     first.M = std::min(p->M, dlk::gemm::kMaxRows);
-    return dlk::gemm::wide_eligible(first) ? 0 : 1;
+    return dlk::gemm::wide_eligible(first) || dlk::gemm::wide_parts_eligible(first) ? 0 : 1;
 }
 
 extern "C" int64_t dlk_gemv_split_floats(const dlk_gemv_params* p) {
@@ -249,7 +253,8 @@ extern "C" int64_t dlk_gemv_split_floats(const dlk_gemv_params* p) {
 
 extern "C" int dlk_gemv_split_count(const dlk_gemv_params* p) {
     using namespace dlk::gemm;
-    if (dlk::tiles::eligible(*p) || !eligible(*p) || p->M > kMaxRows || wide_eligible(*p)) return 1;
+    if (dlk::tiles::eligible(*p) || !eligible(*p) || p->M > kMaxRows || wide_eligible(*p) || wide_parts_eligible(*p))
+        return 1;
     int splits = splits_of(*p, p->M);
     if (splits > 1 && (!p->split_partial || p->split_capacity < split_floats(*p, splits, p->M))) splits = 1;
     if (splits > 1 && split_floats(*p, kMaxSplits, p->M) * 4 > INT32_MAX) splits = 1;
