@@ -66,16 +66,16 @@ inline int row_tiles(int rows) { return rows <= 16 ? 1 : rows <= 32 ? 2 : 4; }
 
 /// Key slices of a launch: one, unless the weight tiles leave most CUs idle; then the most slices (each a whole
 /// number of chunks; runs of one to four chunks take the up-front variant, longer ones the loop) that keep the
-/// launch within 256 work-groups, one per CU.  Measured on MI355X at batch 32 (1B widths):
-/// two work-groups on a CU, each with all of its loads in flight, stream slower than one (gate/up: 24.8 us at
-/// 352 work-groups, 21.0 at 176).
+/// launch within 352 work-groups.  Measured on MI355X (1B widths, SwiGLU, weights repacked): at batch 4,
+/// 16.4 us at 352 work-groups against 17.3 at 176; at batch 32 two work-groups on a CU streamed slower than
+/// one (24.8 us at 352 against 21.0 at 176, row-major weights), and that launch now splits over rows instead.
 inline int splits_of(const dlk_gemv_params& p, int rows) {
     if (p.epilogue == DLK_EPI_LOGITS) return 1;
     const int blocks = blocks_of(p);
     if (blocks >= 192) return 1;
     const int chunks = p.K / chunk_k(row_tiles(rows));
     int best = 1;
-    for (int s = 2; s <= kMaxSplits && blocks * s <= 256; ++s) {
+    for (int s = 2; s <= kMaxSplits && blocks * s <= 352; ++s) {
         if (chunks % s == 0) best = s;
     }
     return best;
