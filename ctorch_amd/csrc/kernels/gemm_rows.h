@@ -682,7 +682,17 @@ __global__ __launch_bounds__(kWideWaves * kWave) void gemm_wide(const dlk_gemv_p
     const int per = K / kWideWaves, steps = per / 32, kb = wave * per;
     const TileMap tm = locate<SWIGLU>(p, tile);
     const int i16 = lane % 16, g4 = lane / 16;
+    // weights row-major (16 rows x 64 bytes per load instruction) or repacked in tile order (w_tiles: 1 KB)
+    const uint16_t* wtiles = static_cast<const uint16_t*>(tm.seg == 0   ? p.w_tiles[0]
+                                                          : tm.seg == 1 ? p.w_tiles[1]
+                                                                        : p.w_tiles[2]);
     const uint16_t* wrow = tile_row<SWIGLU>(tm, i16, K) + kb + 8 * g4;
+    int wstep = 32;
+    if (wtiles) {
+        const int local = SWIGLU ? tm.n0 / 8 : tm.n0 / kTile; // the tile within its segment
+        wrow = wtiles + (static_cast<int64_t>(local) * (K / 32) + kb / 32) * 512 + 8 * lane;
+        wstep = 512;
+    }
     const bool norm = NORM && p.apply_norm;
     const bool affine = norm && p.norm_weight;
     const int esize = p.norm_bf16 ? 2 : 4;
@@ -707,7 +717,7 @@ __global__ __launch_bounds__(kWideWaves * kWave) void gemm_wide(const dlk_gemv_p
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int s = min(s0 + d, steps - 1);
-            wv[d] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + 32 * s));
+            wv[d] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + wstep * s));
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 xv[d][mt][0] = *reinterpret_cast<const float4*>(xrow[mt] + 32 * s);

@@ -238,10 +238,8 @@ extern "C" int dlk_pack_tiles(const void* w0, const void* w1, int swiglu, int64_
 }
 
 extern "C" int dlk_gemv_uses_rows(const dlk_gemv_params* p) {
-    if (dlk::tiles::eligible(*p) || !dlk::gemm::eligible(*p)) return 0;
-    dlk_gemv_params first = *p; // the first launch of kMaxRows rows decides between the wide and the rows kernel
-    first.M = std::min(p->M, dlk::gemm::kMaxRows);
-    return dlk::gemm::wide_eligible(first) || dlk::gemm::wide_parts_eligible(first) ? 0 : 1;
+    // both matrix-core kernels of the batched path (gemm_rows, gemm_wide) read the repacked weights
+    return !dlk::tiles::eligible(*p) && dlk::gemm::eligible(*p) ? 1 : 0;
 }
 
 extern "C" int64_t dlk_gemv_split_floats(const dlk_gemv_params* p) {

@@ -107,7 +107,8 @@ typedef struct dlk_gemv_params {
    tile t interleaves gate and up rows 8 t .. +8 (tile row 2 j: gate 8 t + j, 2 j + 1: up 8 t + j).  out holds
    rows * K (swiglu: 2 * rows * K) bf16. */
 int dlk_pack_tiles(const void* w0, const void* w1, int swiglu, int64_t rows, int64_t K, void* out, dlh_stream stream);
-/* 1 when dlk_gemv takes the batched matrix-core kernel (gemm_rows, the one that reads w_tiles) for this launch. */
+/* 1 when dlk_gemv takes a batched matrix-core kernel (gemm_rows or gemm_wide, which read w_tiles) for this
+   launch. */
 int dlk_gemv_uses_rows(const dlk_gemv_params* p);
 /* Floats of workspace that lets dlk_gemv split the keys of this launch (0 when it would not split). */
 int64_t dlk_gemv_split_floats(const dlk_gemv_params* p);
