@@ -68,14 +68,15 @@ const void* DecodeWorkspace::tiles_of(const Tensor& w0, const Tensor* w1, dlh_st
         packed_.clear();
         packed_epoch_ = epoch;
     }
-    const void* key = w0.data<void>();
+    const PackKey key{w0.data<void>(), rows, K, w1 ? w1->data<void>() : nullptr};
     const auto it = packed_.find(key);
-    if (it != packed_.end() && it->second.source.data<void>() == key) return it->second.tiles.data<void>();
+    if (it != packed_.end()) return it->second.tiles.data<void>();
     if (capturing) return nullptr;
     Tensor tiles = empty_tensor({(w1 ? 2 : 1) * rows * K}, DType::bf16, w0.device());
-    hip_check(dlk_pack_tiles(key, w1 ? w1->data<void>() : nullptr, w1 ? 1 : 0, rows, K, mutable_data(tiles), stream),
+    hip_check(dlk_pack_tiles(w0.data<void>(), w1 ? w1->data<void>() : nullptr, w1 ? 1 : 0, rows, K,
+                             mutable_data(tiles), stream),
               "weight repack");
-    packed_[key] = Packed{w0, tiles};
+    packed_[key] = Packed{w0, w1 ? *w1 : Tensor(), tiles};
     return tiles.data<void>();
 }
 

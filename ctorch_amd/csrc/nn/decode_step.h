@@ -8,7 +8,8 @@
 
 #include <cstdint>
 #include <functional>
-#include <unordered_map>
+#include <map>
+#include <tuple>
 #include <utility>
 
 namespace dl::detail {
@@ -40,9 +41,12 @@ struct DecodeWorkspace {
 
 private:
     struct Packed {
-        Tensor source, tiles; // source keeps the weight's storage (the key) alive while the pack exists
+        Tensor source, second, tiles; // the sources keep the weights' storage (the key) alive while the pack exists
     };
-    std::unordered_map<const void*, Packed> packed_;
+    // a pack is found by everything that shapes it: w0's address, rows and K, and w1's address (gate/up), so a
+    // view at the same address with another shape, or w0 paired with another w1, makes a pack of its own
+    using PackKey = std::tuple<const void*, Index, Index, const void*>;
+    std::map<PackKey, Packed> packed_;
     uint64_t packed_epoch_ = 0;
 };
 

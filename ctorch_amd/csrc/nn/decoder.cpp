@@ -193,6 +193,7 @@ Tensor GroupedQueryAttention::run(const Tensor& input, KVCache* cache) {
         throw std::invalid_argument("attention input must be [batch, length, dimensions]");
     KVCache local(std::max<Index>(1, input.size(1)));
     KVCache& target = cache ? *cache : local;
+    target.check_layout(input.size(0), kv_heads_, head_dim(), cache_dtype_, input.device());
     GpuContext& context = gpu_of(input, "GroupedQueryAttention");
     const Index B = input.size(0), L = input.size(1), d = dimensions_;
     const Index offset = target.length();
@@ -304,6 +305,8 @@ Tensor TransformerDecoderLayer::forward(const Tensor& input) {
 Tensor TransformerDecoderLayer::decode(const Tensor& input, KVCache& cache) {
     if (input.ndim() != 3 || input.size(2) != attention_->dimensions())
         throw std::invalid_argument("decoder layer input must be [batch, length, dimensions]");
+    cache.check_layout(input.size(0), attention_->kv_heads(), attention_->head_dim(), cache_dtype(*this),
+                       input.device());
     GpuContext& context = gpu_of(input, "TransformerDecoderLayer");
     const Index B = input.size(0), L = input.size(1), d = attention_->dimensions();
     if (L > cache.capacity() - cache.length())
@@ -363,6 +366,9 @@ Tensor TransformerDecoder::decode(const Tensor& input, std::span<KVCache> cache)
         if (layer.length() != prefix) throw std::invalid_argument("decoder cache positions differ");
     if (input.ndim() != 3 || input.size(2) != layers_.front()->attention().dimensions())
         throw std::invalid_argument("decoder input must be [batch, length, dimensions]");
+    for (std::size_t i = 0; i < layers_.size(); ++i)
+        cache[i].check_layout(input.size(0), layers_[i]->attention().kv_heads(), layers_[i]->attention().head_dim(),
+                              detail::cache_dtype(*layers_[i]), input.device());
     GpuContext& context = gpu_of(input, "TransformerDecoder");
     const Index B = input.size(0), L = input.size(1), d = input.size(2);
     // every layer's append is checked before anything is launched: a chunk that does not fit leaves all

@@ -22,13 +22,22 @@ void KVCache::sync_position() const {
               "KV cache length");
 }
 
-void KVCache::reserve(Index batch, Index heads, Index head_dim, DType dtype, Device device) {
+void KVCache::check_layout(Index batch, Index heads, Index head_dim, DType dtype, Device device) const {
+    if (!key_) return;
+    // the fused kernels write and read both tensors with the layer's shape and dtype: a cache whose key or
+    // value storage (each taken from its own first append) differs must fail here, before any launch
     const Shape shape{batch, heads, capacity_, head_dim};
-    if (key_) {
-        if (key_->shape() != shape || key_->dtype() != dtype || !(key_->device() == device))
-            throw std::invalid_argument("KV cache shape, dtype or device changed");
-        return;
-    }
+    auto differs = [&](const std::optional<Tensor>& storage) {
+        return !storage || storage->shape() != shape || storage->dtype() != dtype || !(storage->device() == device);
+    };
+    if (differs(key_) || differs(value_) || (device.type == DeviceType::gpu && !position_))
+        throw std::invalid_argument("KV cache shape, dtype or device changed");
+}
+
+void KVCache::reserve(Index batch, Index heads, Index head_dim, DType dtype, Device device) {
+    check_layout(batch, heads, head_dim, dtype, device);
+    if (key_) return;
+    const Shape shape{batch, heads, capacity_, head_dim};
     key_ = empty_tensor(shape, dtype, device);
     value_ = empty_tensor(shape, dtype, device);
     if (device.type == DeviceType::gpu) {

@@ -49,8 +49,10 @@ void DecoderLM::check_caches(std::span<nn::KVCache> cache, Index batch, Index le
             throw std::invalid_argument("KV cache append exceeds capacity or has unequal key/value lengths");
         if (prefix + length > decoder_->layer(static_cast<Index>(i)).attention().rotary().cosine().size(0))
             throw std::out_of_range("RoPE positions exceed the table capacity");
+        const auto& layer = decoder_->layer(static_cast<Index>(i));
+        cache[i].check_layout(batch, layer.attention().kv_heads(), layer.attention().head_dim(), cache_dtype(layer),
+                              embedding_->weight().device());
     }
-    (void)batch;
 }
 
 void DecoderLM::forward_chunk(const Index* ids, Index batch, Index length, std::span<nn::KVCache> cache,

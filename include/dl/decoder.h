@@ -95,6 +95,10 @@ public:
     /// Allocates [batch, heads, capacity, head_dim] storage of `dtype` on `device` if absent (a no-op when
     /// the same layout already exists; throws if it differs).  Used by the fused decode path.
     void reserve(Index batch, Index heads, Index head_dim, DType dtype, Device device);
+    /// Throws std::invalid_argument unless reserve() with these arguments would succeed: no storage yet, or
+    /// key and value storage both of exactly this layout.  Allocates nothing; the fused paths call it for every
+    /// layer before their first launch.
+    void check_layout(Index batch, Index heads, Index head_dim, DType dtype, Device device) const;
     bool reserved() const { return key_.has_value(); }
     /// Device pointers for kernels (valid after reserve on a GPU).
     void* key_data() const;

@@ -103,3 +103,32 @@ def test_cache_state_is_a_snapshot_of_a_full_f32_cache():
     assert np.array_equal(cache.state()["past_key_0"].numpy(), other["past_key_0"])
     for name, want in first.items():
         assert np.array_equal(exported[name].numpy(), want), name
+
+
+def test_decode_refuses_a_cache_whose_value_storage_differs_before_any_launch():
+    """KV storage takes its shape and dtype from its first append, separately for keys and values (as the
+    reference's does).  The fused decode writes and reads both with the layer's layout, so a cache whose value
+    storage differs in dtype or head size must be refused on the host before anything is launched: here the
+    decoder lives on the host, and the refusal must come from the cache check, not from the missing GPU."""
+    cpu = ct.device("cpu")
+    rng = np.random.default_rng(9)
+    dec = ct.transformer_decoder(2, 64, 4, 2, 96, 24, ct.F32, cpu)
+    x = ct.Tensor.from_numpy(rng.standard_normal((1, 1, 64)).astype(np.float32), ct.F32, cpu)
+    key = rng.standard_normal((1, 2, 3, 16)).astype(np.float32)
+    mixed_dtype = (ct.Tensor.from_numpy(key, ct.F32, cpu), ct.Tensor.from_numpy(oracle.bf16_encode(key), ct.BF16, cpu))
+    wide_value = (ct.Tensor.from_numpy(key, ct.F32, cpu),
+                  ct.Tensor.from_numpy(rng.standard_normal((1, 2, 3, 32)).astype(np.float32), ct.F32, cpu))
+    for k, v in (mixed_dtype, wide_value):
+        cache = ct.DecoderCache(dec)
+        for layer in range(2):
+            cache.append(layer, k, v)
+        with pytest.raises(ct.DLError, match="KV cache shape, dtype or device changed"):
+            ct.decode(dec, x, cache)
+        assert cache.length == 3
+    # a consistent cache passes the check and fails only where compute begins (no host compute path)
+    cache = ct.DecoderCache(dec)
+    for layer in range(2):
+        cache.append(layer, ct.Tensor.from_numpy(key, ct.F32, cpu), ct.Tensor.from_numpy(key, ct.F32, cpu))
+    with pytest.raises(ct.DLError) as raised:
+        ct.decode(dec, x, cache)
+    assert "KV cache" not in str(raised.value)
