@@ -140,6 +140,9 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const dlk_attention
 #pragma unroll
                 for (int d = 0; d < HD; ++d) acc += q_tile[r][d] * KvTraits<KT>::at(krow, d);
                 s = acc;
+                if (p.keep_mask && !p.keep_mask[b * p.mask_stride[0] + row_h(r) * p.mask_stride[1] +
+                                                row_l(r) * p.mask_stride[2] + kk * p.mask_stride[3]])
+                    s = -INFINITY;
             }
             const float tile_max = wave_max(s);
             const float m_new = fmaxf(m_run[j], tile_max);
@@ -178,7 +181,8 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(const dlk_attention
         const int l = row_l(r), h = row_h(r);
         const int64_t m = static_cast<int64_t>(b) * p.L + l;
         if (p.splits == 1) {
-            const float inv = l_run[j] > 0.0f ? 1.0f / l_run[j] : 0.0f;
+            // a masked row that kept no key: NaN, as the reference's softmax over an all -inf row
+            const float inv = l_run[j] > 0.0f ? 1.0f / l_run[j] : p.keep_mask ? __builtin_nanf("") : 0.0f;
 #pragma unroll
             for (int c = 0; c < DCOLS; ++c) {
                 const int d = lane + c * kWave;
@@ -257,7 +261,7 @@ __global__ __launch_bounds__(kCombineThreads) void attention_combine(const dlk_a
             sum += acc_s[g][d];
             weight += total_s[g];
         }
-        const float inv = weight > 0.0f ? 1.0f / weight : 0.0f;
+        const float inv = weight > 0.0f ? 1.0f / weight : p.keep_mask ? __builtin_nanf("") : 0.0f;
         p.out[(b * p.L + l) * p.ldo + h * HD + d] = sum * inv;
     }
 }
@@ -294,16 +298,19 @@ __global__ __launch_bounds__(kWave) void attention_small(const dlk_attention_par
     float m = -INFINITY, total = 0.0f, o[HD];
 #pragma unroll
     for (int d = 0; d < HD; ++d) o[d] = 0.0f;
+    const unsigned char* keep =
+        p.keep_mask ? p.keep_mask + b * p.mask_stride[0] + h * p.mask_stride[1] + l * p.mask_stride[2] : nullptr;
     for (int64_t k0 = k_begin; k0 < k_end; k0 += kWave) {
         const int64_t key = k0 + lane;
-        const bool live = key < k_end;
+        // a live key the mask keeps (without a mask every step holds one, so m_new is finite)
+        const bool live = key < k_end && (!keep || keep[key * p.mask_stride[3]]);
         float s = -INFINITY;
         if (live) {
             s = 0.0f;
 #pragma unroll
             for (int d = 0; d < HD; ++d) s += q[d] * value(kbase + key * HD, d);
         }
-        const float m_new = fmaxf(m, wave_max(s)); // finite: every step holds at least one live key
+        const float m_new = fmaxf(m, wave_max(s));
         const float alpha = m == -INFINITY ? 0.0f : expf(m - m_new);
         const float pr = live ? expf(s - m_new) : 0.0f;
         total = total * alpha + wave_sum(pr);
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(kWave) void attention_small(const dlk_attention_par
     if (p.splits == 1) {
         float* out = p.out + (static_cast<int64_t>(b) * p.L + l) * p.ldo + static_cast<int64_t>(h) * HD;
 #pragma unroll
-        for (int d = 0; d < HD; ++d) out[d] = total > 0.0f ? o[d] / total : 0.0f;
+        for (int d = 0; d < HD; ++d) out[d] = total > 0.0f ? o[d] / total : keep ? __builtin_nanf("") : 0.0f;
     } else {
         const int64_t slot = prow * p.splits + split;
 #pragma unroll
@@ -398,6 +405,8 @@ extern "C" int dlk_attention(const dlk_attention_params* params, dlh_stream stre
     if (p.B <= 0 || p.L <= 0 || p.KV <= 0 || p.H % p.KV != 0 || p.splits <= 0 || p.chunk <= 0 ||
         (p.splits > 1 && (!p.partial_o || !p.partial_ml)) || (p.splits > 1 && p.chunk % 64 != 0))
         return static_cast<int>(hipErrorInvalidValue);
+    // a keep mask is applied by the general and small-head kernels, which serve non-causal attention
+    if (p.keep_mask && (p.causal || p.qkv_partial || p.stage_out || p.kv_split)) return static_cast<int>(hipErrorInvalidValue);
     // the QKV projection's partials are finished only by the matrix kernel
     if (p.qkv_partial && (p.stage_out || !dlk_attention_matrix_eligible(&p))) return static_cast<int>(hipErrorInvalidValue);
     // the staged output exists only on the prefill kernel

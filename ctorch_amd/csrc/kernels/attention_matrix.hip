@@ -509,7 +509,8 @@ extern "C" int dlk_attention_matrix_eligible(const dlk_attention_params* p) {
                      (p->qkv_splits >= 1 && p->qkv_splits <= 16 && p->rope_cos && p->rope_sin && p->qkv_K > 0 &&
                       p->qkv_width == (p->H + 2 * p->KV) * p->hd &&
                       24LL * p->B * p->qkv_width * 4 <= INT32_MAX);
-    return p->L == 1 && dlk_attention_matrix_heads(p->H, p->KV, p->hd) && p->chunk % (4 * dlk::kTileKeys) == 0 &&
+    return p->L == 1 && !p->keep_mask && dlk_attention_matrix_heads(p->H, p->KV, p->hd) &&
+           p->chunk % (4 * dlk::kTileKeys) == 0 &&
            p->ldq % 4 == 0 && qkv &&
            (p->splits == 1 || (p->partial_o && p->partial_ml));
 }

@@ -490,7 +490,7 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
 /* Whether dlk_attention takes the matrix-core prefill kernel for these parameters. */
 extern "C" int dlk_attention_prefill_eligible(const dlk_attention_params* p) {
     const int G = p->KV > 0 ? p->H / p->KV : 0;
-    return p->causal && (p->hd == 64 || p->hd == 128) && p->L >= 16 && G > 0 && dlk::kRows % G == 0 &&
+    return p->causal && !p->keep_mask && (p->hd == 64 || p->hd == 128) && p->L >= 16 && G > 0 && dlk::kRows % G == 0 &&
            p->splits == 1 && p->ldq % 4 == 0 && p->ldo % 4 == 0;
 }
 

@@ -168,6 +168,14 @@ typedef struct dlk_attention_params {
                                 launch splits the live K/V tiles into bf16 hi + lo planes once, and the attention
                                 copies them into LDS as they are instead of splitting each tile it reads */
     int kv_split_tiles;
+    /* Explicit keep mask (reference grouped_query_attention, src/ops/attention.cpp:48-50,156-183), or NULL: bool
+       bytes, key s of query row (b, h, l) kept when keep_mask[b * mask_stride[0] + h * mask_stride[1] +
+       l * mask_stride[2] + s * mask_stride[3]] is nonzero (element strides, 0 on broadcast axes).  A dropped key's
+       score is -inf before the softmax, and a row that keeps no key comes out NaN, as the reference's softmax of
+       an all -inf row does.  Taken by the general and small-head kernels only (not causal, not the matrix-core or
+       prefill kernels). */
+    const unsigned char* keep_mask;
+    int64_t mask_stride[4];
 } dlk_attention_params;
 
 /* Keys per split of a short one-position decode over a bf16 cache (few keys in all): 256 or 512, one work-group. */

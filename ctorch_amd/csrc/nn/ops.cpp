@@ -211,7 +211,6 @@ Tensor rotary_embedding(const Tensor& input, const Tensor& cosine, const Tensor&
 Tensor grouped_query_attention(const Tensor& query, const Tensor& key, const Tensor& value,
                                std::optional<Tensor> keep_mask) {
     GpuContext& context = gpu_of(query, "grouped_query_attention");
-    if (keep_mask) throw std::invalid_argument("grouped_query_attention: explicit keep masks are not supported on the GPU path");
     if (query.ndim() != 4 || key.ndim() != 4 || value.ndim() != 4)
         throw std::invalid_argument("grouped_query_attention: expects [B,H,L,D] and [B,KV,S,D]");
     const Index B = query.size(0), H = query.size(1), L = query.size(2), D = query.size(3);
@@ -240,6 +239,30 @@ Tensor grouped_query_attention(const Tensor& query, const Tensor& key, const Ten
     p.out = static_cast<float*>(mutable_data(out));
     p.ldo = H * D;
     if (S < L) throw std::invalid_argument("grouped_query_attention: needs S >= L");
+    // The keep mask, as the reference applies it (src/ops/attention.cpp:48-50,80,156-183): a bool tensor that
+    // broadcasts to [B, H, L, S] by the trailing-axis rule; the kernels read it in place through its strides
+    // (0 on the broadcast axes), on the query's device
+    Tensor mask;
+    if (keep_mask) {
+        if (keep_mask->dtype() != DType::boolean)
+            throw std::invalid_argument("grouped_query_attention: keep mask must be bool");
+        mask = keep_mask->device() == query.device() ? *keep_mask : keep_mask->to(query.device());
+        const Shape want{B, H, L, S};
+        const Index rank = mask.ndim();
+        for (Index axis = 0; axis + 4 < rank; ++axis)
+            if (mask.size(axis) != 1)
+                throw std::invalid_argument("grouped_query_attention: keep mask " + shape_string(mask.shape()) +
+                                            " does not broadcast to " + shape_string(want));
+        for (int axis = 0; axis < 4; ++axis) {
+            const Index from = rank - 4 + axis; // the mask axis aligned with output axis `axis`, if any
+            const Index size = from >= 0 ? mask.size(from) : 1;
+            if (size != 1 && size != want[axis])
+                throw std::invalid_argument("grouped_query_attention: keep mask " + shape_string(mask.shape()) +
+                                            " does not broadcast to " + shape_string(want));
+            p.mask_stride[axis] = size == 1 ? 0 : mask.strides()[static_cast<std::size_t>(from)];
+        }
+        p.keep_mask = static_cast<const unsigned char*>(mask.data<void>());
+    }
     attention_split(B, H, KV, D, kv_dtype == DType::bf16, L, S, p.splits, p.chunk);
     Tensor po, pml;
     if (p.splits > 1) {

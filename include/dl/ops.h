@@ -15,7 +15,10 @@ DL_API Tensor argmax(const Tensor& input, Index axis, KeepDim keep = KeepDim::no
 DL_API Tensor rotary_embedding(const Tensor& input, const Tensor& cosine, const Tensor& sine);
 /// Q [B,H,L,D], K [B,KV,S,D], V [B,KV,S,D]; query head h reads KV head h / (H/KV).  With no mask every query
 /// row sees all S keys, as in the reference (src/ops/attention.cpp:161-164: no causal window); the decoder's
-/// causal rule is applied by its own layers.  An explicit keep mask is not supported (throws).
+/// causal rule is applied by its own layers.  An explicit keep mask (reference include/dl/ops.h:149-153,
+/// src/ops/attention.cpp:48-50,156-183) is a bool tensor broadcast to [B,H,L,S] by the trailing-axis rule: a
+/// false entry drops that key from that row's softmax (its score becomes -inf), and a row that keeps no key
+/// comes out NaN, as the reference's softmax of an all -inf row does.  Masked calls take the general kernels.
 DL_API Tensor grouped_query_attention(const Tensor& query, const Tensor& key, const Tensor& value,
                                       std::optional<Tensor> keep_mask = std::nullopt);
 /// input [..., in] times weight [out, in]^T (+ bias [out]).

@@ -91,6 +91,7 @@ def _declare(L):
     L.orc_silu.argtypes = [C.c_float]
     L.orc_silu.restype = C.c_float
     L.orc_attention.argtypes = [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]
+    L.orc_attention_masked.argtypes = [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]
     L.orc_log.argtypes = [_f64]
     L.orc_log.restype = _f64
     L.orc_gumbel.argtypes = [_u64, _u64, _u64]
@@ -217,15 +218,31 @@ def silu(v: float) -> float:
     return float(lib().orc_silu(v))
 
 
-def attention(q, k, v, causal_first: int = -1) -> np.ndarray:
-    """q [B,H,L,hd]; k,v [B,KV,S,hd] (contiguous); returns [B,H,L,hd]."""
+def attention(q, k, v, causal_first: int = -1, keep_mask=None) -> np.ndarray:
+    """q [B,H,L,hd]; k,v [B,KV,S,hd] (contiguous); returns [B,H,L,hd].  keep_mask: bool array broadcastable to
+    [B,H,L,S] (numpy rules, as the reference's where), False dropping a key from the softmax."""
     q = np.ascontiguousarray(q, np.float32)
     k = np.ascontiguousarray(k, np.float32)
     v = np.ascontiguousarray(v, np.float32)
     B, H, L, hd = q.shape
     KV, S = k.shape[1], k.shape[2]
     out = np.empty_like(q)
-    lib().orc_attention(_ptr(q), _ptr(k), _ptr(v), B, H, KV, L, S, S, hd, causal_first, _ptr(out))
+    if keep_mask is None:
+        lib().orc_attention(_ptr(q), _ptr(k), _ptr(v), B, H, KV, L, S, S, hd, causal_first, _ptr(out))
+        return out
+    mask = np.ascontiguousarray(np.asarray(keep_mask, dtype=bool)).view(np.uint8)
+    if mask.ndim > 4:
+        raise ValueError("keep mask rank above 4")
+    shape = (1,) * (4 - mask.ndim) + mask.shape
+    mask = mask.reshape(shape)
+    strides = []
+    for axis, (size, want) in enumerate(zip(shape, (B, H, L, S))):
+        if size not in (1, want):
+            raise ValueError(f"keep mask {shape} does not broadcast to {(B, H, L, S)}")
+        strides.append(0 if size == 1 else mask.strides[axis])
+    st = np.array(strides, dtype=np.int64)
+    lib().orc_attention_masked(_ptr(q), _ptr(k), _ptr(v), B, H, KV, L, S, S, hd, causal_first, _ptr(mask), _ptr(st),
+                               _ptr(out))
     return out
 
 

@@ -359,6 +359,7 @@ float orc_silu(float v) {
 
 typedef struct {
     const float *q, *k, *v; int64_t batch, heads, kv_heads, length, source, kv_stride, head_dim, first; float* out;
+    const uint8_t* mask; const int64_t* mask_strides;
 } attention_job;
 
 static void attention_range(int64_t begin, int64_t end, void* context) {
@@ -379,6 +380,14 @@ static void attention_range(int64_t begin, int64_t end, void* context) {
             for (int64_t d = 0; d < hd; ++d) acc += q[d] * keys[s * hd + d];
             scores[s] = acc * scale;
         }
+        /* keep mask (src/ops/attention.cpp:48-50,80): where(mask, scores * scale, -inf), the mask read through
+           its broadcast strides over [B, H, L, S] */
+        if (job->mask) {
+            const int64_t* st = job->mask_strides;
+            const uint8_t* row = job->mask + b * st[0] + h * st[1] + l * st[2];
+            for (int64_t s = 0; s < S; ++s)
+                if (!row[s * st[3]]) scores[s] = -INFINITY;
+        }
         if (job->first >= 0 && job->first < S - 1) {
             for (int64_t s = job->first + l + 1; s < S; ++s) scores[s] = -INFINITY;
         }
@@ -397,7 +406,15 @@ static void attention_range(int64_t begin, int64_t end, void* context) {
 void orc_attention(const float* q, const float* k, const float* v, int64_t batch, int64_t heads, int64_t kv_heads,
                    int64_t length, int64_t source, int64_t kv_stride, int64_t head_dim, int64_t causal_first,
                    float* out) {
-    attention_job job = {q, k, v, batch, heads, kv_heads, length, source, kv_stride, head_dim, causal_first, out};
+    orc_attention_masked(q, k, v, batch, heads, kv_heads, length, source, kv_stride, head_dim, causal_first, NULL,
+                         NULL, out);
+}
+
+void orc_attention_masked(const float* q, const float* k, const float* v, int64_t batch, int64_t heads,
+                          int64_t kv_heads, int64_t length, int64_t source, int64_t kv_stride, int64_t head_dim,
+                          int64_t causal_first, const uint8_t* mask, const int64_t* mask_strides, float* out) {
+    attention_job job = {q, k, v, batch, heads, kv_heads, length, source, kv_stride, head_dim, causal_first, out,
+                         mask, mask_strides};
     parallel_for(batch * heads * length, 4, attention_range, &job);
 }
 

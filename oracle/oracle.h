@@ -82,6 +82,12 @@ float orc_silu(float v);
 void orc_attention(const float* q, const float* k, const float* v, int64_t batch, int64_t heads, int64_t kv_heads,
                    int64_t length, int64_t source, int64_t kv_stride, int64_t head_dim, int64_t causal_first,
                    float* out);
+/* the same with a keep mask (src/ops/attention.cpp:48-50,156-183): bool bytes read at b*st[0] + h*st[1] + l*st[2]
+ * + s*st[3] (strides in elements, 0 on broadcast axes); a dropped key's scaled score becomes -inf before the
+ * softmax, so a row that keeps no key comes out NaN (the reference softmax over an all -inf row) */
+void orc_attention_masked(const float* q, const float* k, const float* v, int64_t batch, int64_t heads,
+                          int64_t kv_heads, int64_t length, int64_t source, int64_t kv_stride, int64_t head_dim,
+                          int64_t causal_first, const uint8_t* mask, const int64_t* mask_strides, float* out);
 
 /* ---- sampling (the build's new op; no reference counterpart, see a13) ---- */
 double orc_log(double x);                       /* portable natural log: atanh series, basic IEEE ops only */

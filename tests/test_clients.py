@@ -3,8 +3,9 @@ linked with libctorch_amd.so, with no Python in between.
 
   tests/clients/decode_client.c    C17: the decoder block of the reference's tests/c_api.c:28-42 (on DL_CUDA),
                                    then the greedy loop of examples/decoder_generate.cpp:16-31 over the C surface;
-  tests/clients/decode_client.cpp  C++20: examples/decoder_generate.cpp with its ByteDecoder model class
-                                   (Device::cuda(), NoGradGuard, io::load, from_span, select, argmax().item()).
+  tests/clients/decode_client.cpp  C++20: greedy byte generation through the dl:: C++ API a reference caller
+                                   uses (Device::cuda(), NoGradGuard, io::load, load_state_dict, make_cache,
+                                   decode, from_span, select, argmax().item(), full).
 
 The CPU test compiles both with -Werror; the GPU test runs the programs __graft_entry__.build() built (under
 tests/clients/_build) on a byte decoder whose weights the oracle also evaluates, and requires the oracle's greedy
@@ -79,12 +80,14 @@ def test_c17_client_runs_the_reference_block_and_the_greedy_loop(tmp_path):
 
 
 @pytest.mark.gpu
-def test_cpp20_client_runs_the_reference_generate_loop_on_device_cuda(tmp_path):
-    print("case: C++20 client (examples/decoder_generate.cpp loop with Device::cuda() and NoGradGuard)", flush=True)
+def test_cpp20_client_generates_through_the_cpp_api_on_device_cuda(tmp_path):
+    print("case: C++20 client (dl:: decoder API with Device::cuda() and NoGradGuard)", flush=True)
     ref = byte_decoder_archive(tmp_path / "byte_decoder.ct", root=(304, 0))
     prefix = "tokens per second "
-    out = run_client([os.path.join(BUILT, "decode_client_cpp"), str(tmp_path / "byte_decoder.ct"), prefix, "24",
-                      "cuda"])
-    got = np.array([int(x) for x in out.split() if x])
+    out = run_client([os.path.join(BUILT, "decode_client_cpp"), "--archive", str(tmp_path / "byte_decoder.ct"),
+                      "--prompt", prefix, "--steps", "24", "--device", "cuda"])
+    lines = out.split()
+    assert lines[-1] == f"cache_length={len(prefix) + 23}"
+    got = np.array([int(x) for x in lines[:-1]])
     want, _ = ref.generate(np.frombuffer(prefix.encode(), np.uint8).astype(np.int64).reshape(1, -1), 24)
     assert np.array_equal(got, want[0]), (got, want[0])

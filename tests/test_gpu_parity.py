@@ -122,6 +122,54 @@ def G(array, dtype=None):
     return ct.Tensor.from_numpy(array, dtype, GPU)
 
 
+def test_grouped_query_attention_keep_mask_matches_the_oracle():
+    """dl_grouped_query_attention with an explicit keep mask (reference include/dl/ops.h:149-153,
+    src/ops/attention.cpp:48-50,156-183): a bool mask broadcast to [B, H, L, S], a dropped key's score -inf before
+    the softmax, and a row that keeps no key NaN (the reference softmax of an all -inf row).  Random masks at
+    several broadcast shapes, over f32 and bf16 K/V, one and several positions, key splits merged by the combine
+    launch, head sizes 2 to 128, masks on the GPU and on the host; against the oracle (pinned to torch float64
+    SDPA with the same mask)."""
+    say("case: dl_grouped_query_attention with keep masks")
+    rng = np.random.default_rng(15)
+    cases = [  # B, H, KV, L, S, hd, mask shape
+        (2, 8, 2, 1, 200, 64, (2, 8, 1, 200)), (2, 8, 2, 1, 200, 64, (200,)), (2, 8, 2, 5, 70, 64, (5, 70)),
+        (2, 8, 2, 5, 70, 64, (2, 1, 5, 70)), (1, 32, 8, 1, 2100, 64, (1, 32, 1, 2100)),
+        (3, 4, 4, 7, 33, 128, (3, 4, 7, 33)), (2, 4, 1, 6, 90, 32, (1, 4, 6, 1)), (2, 8, 2, 3, 40, 16, (3, 40)),
+        (2, 4, 2, 4, 20, 2, (2, 4, 4, 20)), (1, 2, 1, 3, 150, 8, (3, 150)), (8, 8, 2, 1, 3000, 64, (8, 1, 1, 3000)),
+    ]
+    for B, H, KV, L, S, hd, mshape in cases:
+        qq = rng.standard_normal((B, H, L, hd)).astype(np.float32)
+        kk = rng.standard_normal((B, KV, S, hd)).astype(np.float32)
+        vv = rng.standard_normal((B, KV, S, hd)).astype(np.float32)
+        mask = rng.random(mshape) < 0.7
+        if mask.size // mshape[-1] > 1:
+            mask.reshape(-1, mshape[-1])[-1] = False  # a row (or the rows it broadcasts to) that keeps no key
+        kb, vb = oracle.bf16_encode(kk), oracle.bf16_encode(vv)
+        for kv_dtype in (ct.F32, ct.BF16):
+            k_in = kk if kv_dtype == ct.F32 else kb
+            v_in = vv if kv_dtype == ct.F32 else vb
+            kf = kk if kv_dtype == ct.F32 else oracle.bf16_decode(kb)
+            vf = vv if kv_dtype == ct.F32 else oracle.bf16_decode(vb)
+            want = oracle.attention(qq, kf, vf, keep_mask=mask)
+            for where in (GPU, ct.device("cpu")):
+                m = ct.Tensor.from_numpy(mask, ct.BOOL, where)
+                got = ct.grouped_query_attention(G(qq), G(k_in, kv_dtype), G(v_in, kv_dtype), m).numpy()
+                case = (B, H, KV, L, S, hd, mshape, kv_dtype)
+                assert np.array_equal(np.isnan(got), np.isnan(want)), case
+                live = ~np.isnan(want)
+                assert np.max(np.abs(got[live] - want[live])) <= 2e-5, case
+        # a mask of all True equals no mask
+        full = ct.Tensor.from_numpy(np.ones(mshape, bool), ct.BOOL, GPU)
+        got = ct.grouped_query_attention(G(qq), G(kk), G(vv), full).numpy()
+        assert np.max(np.abs(got - oracle.attention(qq, kk, vv))) <= 2e-5
+    qq = rng.standard_normal((2, 8, 3, 64)).astype(np.float32)
+    kk = rng.standard_normal((2, 2, 9, 64)).astype(np.float32)
+    with pytest.raises(ct.DLError, match="must be bool"):
+        ct.grouped_query_attention(G(qq), G(kk), G(kk), G(np.ones((3, 9), np.float32)))
+    with pytest.raises(ct.DLError, match="does not broadcast"):
+        ct.grouped_query_attention(G(qq), G(kk), G(kk), ct.Tensor.from_numpy(np.ones((4, 9), bool), ct.BOOL, GPU))
+
+
 def test_operators_match_the_oracle():
     say("case: dl_linear / dl_rms_norm / dl_embedding / dl_rotary_embedding / dl_grouped_query_attention")
     rng = np.random.default_rng(5)

@@ -236,6 +236,39 @@ def test_grouped_attention_vs_torch_float64(L, first):
     assert np.max(np.abs(out - ref)) < 2e-6
 
 
+@pytest.mark.parametrize("mask_shape", [(2, 8, 5, 13), (2, 1, 5, 13), (5, 13), (13,), (2, 8, 1, 13), (1, 1, 1, 1),
+                                        (1, 8, 5, 1)])
+def test_masked_grouped_attention_vs_torch_float64(mask_shape):
+    """The keep mask of grouped_query_attention (reference src/ops/attention.cpp:48-50,156-183): broadcast to
+    [B, H, L, S], a dropped key's score -inf before the softmax.  Rows that keep a key are pinned against torch's
+    float64 SDPA with the same boolean attn_mask; a row that keeps none comes out NaN, which is what the
+    reference's softmax of an all -inf row gives (exp(-inf - -inf)), and what torch's explicit softmax gives too
+    (its SDPA returns 0 there instead, so those rows are pinned against the explicit form)."""
+    rng = np.random.default_rng(11)
+    B, H, KV, L, S, hd = 2, 8, 2, 5, 13, 32
+    q = rng.standard_normal((B, H, L, hd)).astype(np.float32)
+    k = rng.standard_normal((B, KV, S, hd)).astype(np.float32)
+    v = rng.standard_normal((B, KV, S, hd)).astype(np.float32)
+    mask = rng.random(mask_shape) < 0.6
+    if mask.size // mask_shape[-1] > 1:
+        mask.reshape(-1, mask_shape[-1])[0] = False  # one row (or every row it broadcasts to) keeps no key
+    out = oracle.attention(q, k, v, keep_mask=mask)
+    G = H // KV
+    kk = torch.from_numpy(k).double().repeat_interleave(G, dim=1)
+    vv = torch.from_numpy(v).double().repeat_interleave(G, dim=1)
+    qq = torch.from_numpy(q).double()
+    mm = torch.from_numpy(np.broadcast_to(mask, (B, H, L, S)).copy())
+    sdpa = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, attn_mask=mm).numpy()
+    scores = (qq @ kk.transpose(-1, -2)) / math.sqrt(hd)
+    explicit = (torch.softmax(scores.masked_fill(~mm, float("-inf")), -1) @ vv).numpy()
+    kept = mm.any(-1).numpy()
+    if kept.any():
+        assert np.max(np.abs(out[kept] - sdpa[kept])) < 2e-6
+    assert np.isnan(explicit[~kept]).all() and np.isnan(out[~kept]).all()
+    if mask.all():
+        assert np.array_equal(out, oracle.attention(q, k, v))
+
+
 # ------------------------------------------------------------------------------------------ sampler
 def test_portable_log_matches_libm():
     rng = np.random.default_rng(8)
