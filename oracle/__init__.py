@@ -387,6 +387,19 @@ class OracleLM:
             raise ValueError(f"oracle lm failed with status {st}")
         return out
 
+    def last_logits(self, ids: np.ndarray, cache: "OracleCache") -> np.ndarray:
+        """logits(ids, cache)[:, -1] without the head over the other positions: the embedding rows, the decoder
+        (orc_decoder_decode, final RMSNorm included, as orc_lm_logits runs them), then the head on each sequence's
+        last row only (orc_linear)."""
+        ids = np.ascontiguousarray(ids, np.int64)
+        B, L = ids.shape
+        if ids.min() < 0 or ids.max() >= self.cfg.vocab:
+            raise ValueError("token id out of range")
+        table = self.w["tokens.weight"]
+        x = bf16_decode(table[ids]) if self.cfg.dtype == "bf16" else np.asarray(table[ids], np.float32)
+        features = self.decode(x, cache)
+        return linear(np.ascontiguousarray(features[:, -1]), self.w["output.weight"])
+
     def generate(self, prompt: np.ndarray, steps: int, temperature: float = 0.0, key=(0, 0),
                  cache: "OracleCache | None" = None):
         prompt = np.ascontiguousarray(prompt, np.int64)

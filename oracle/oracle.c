@@ -375,7 +375,17 @@ static void attention_range(int64_t begin, int64_t end, void* context) {
         const float* q = job->q + ((b * job->heads + h) * L + l) * hd;
         const float* keys = job->k + (b * job->kv_heads + kvh) * job->kv_stride * hd;
         const float* values = job->v + (b * job->kv_heads + kvh) * job->kv_stride * hd;
-        for (int64_t s = 0; s < S; ++s) {
+        /* eight scores at a time: each sum runs over d in order, the eight chains side by side */
+        int64_t s0 = 0;
+        for (; s0 + 8 <= S; s0 += 8) {
+            float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            for (int64_t d = 0; d < hd; ++d) {
+                const float qd = q[d];
+                for (int j = 0; j < 8; ++j) acc[j] += qd * keys[(s0 + j) * hd + d];
+            }
+            for (int j = 0; j < 8; ++j) scores[s0 + j] = acc[j] * scale;
+        }
+        for (int64_t s = s0; s < S; ++s) {
             float acc = 0.0f;
             for (int64_t d = 0; d < hd; ++d) acc += q[d] * keys[s * hd + d];
             scores[s] = acc * scale;
@@ -392,11 +402,13 @@ static void attention_range(int64_t begin, int64_t end, void* context) {
             for (int64_t s = job->first + l + 1; s < S; ++s) scores[s] = -INFINITY;
         }
         orc_softmax_row(scores, S, probabilities);
+        /* P V: one sum per head dimension, each over s in order, all of them side by side */
         float* o = job->out + ((b * job->heads + h) * L + l) * hd;
-        for (int64_t d = 0; d < hd; ++d) {
-            float acc = 0.0f;
-            for (int64_t s = 0; s < S; ++s) acc += probabilities[s] * values[s * hd + d];
-            o[d] = acc;
+        for (int64_t d = 0; d < hd; ++d) o[d] = 0.0f;
+        for (int64_t s = 0; s < S; ++s) {
+            const float p = probabilities[s];
+            const float* v = values + s * hd;
+            for (int64_t d = 0; d < hd; ++d) o[d] += p * v[d];
         }
     }
     free(scores);

@@ -6,6 +6,8 @@ decoder.* entries (its RoPE buffers stay the library's own), Linear head from ou
 """
 from __future__ import annotations
 
+import sys
+
 import numpy as np
 
 import ctorch_amd as ct
@@ -70,6 +72,45 @@ def seed_prefix(ref_cache, gpu_cache, layer, keys, values, kv_dtype):
     ref_cache.fill(layer, keys.shape[2], kf, vf)
 
 
+def say(msg):
+    """Progress lines of the GPU tests (flushed: a long case names itself before it runs)."""
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
 def rel_err(got: np.ndarray, want: np.ndarray) -> float:
     """max |got - want| / max |want| over the whole array (the f32 logit criterion)."""
     return float(np.max(np.abs(got.astype(np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def one_block_prefix(ref_cache, gpu_cache, layers, batch, kv_heads, length, head_dim, key, kv_dtype):
+    """The same seeded N(0, 1) K and V block (bf16-exact values) in every layer: appended to the GPU cache in its
+    dtype and written into the oracle's f32 cache."""
+    k = oracle.randn(oracle.fold_in(key, 0), batch * kv_heads * length * head_dim)
+    v = oracle.randn(oracle.fold_in(key, 1), batch * kv_heads * length * head_dim)
+    kb = oracle.bf16_encode(k).reshape(batch, kv_heads, length, head_dim)
+    vb = oracle.bf16_encode(v).reshape(batch, kv_heads, length, head_dim)
+    del k, v
+    kf, vf = oracle.bf16_decode(kb), oracle.bf16_decode(vb)
+    gpu = ct.device("gpu")
+    if kv_dtype == ct.BF16:
+        gk, gv = ct.Tensor.from_numpy(kb, ct.BF16, gpu), ct.Tensor.from_numpy(vb, ct.BF16, gpu)
+    else:
+        gk, gv = ct.Tensor.from_numpy(kf, ct.F32, gpu), ct.Tensor.from_numpy(vf, ct.F32, gpu)
+    for layer in range(layers):
+        # each layer gets its own copy of the block (an append copies into the layer's storage)
+        gpu_cache.append(layer, gk, gv)
+        ref_cache.fill(layer, length, kf, vf)
+
+
+def greedy_steps(ref, gpu, rc, gc, ids, steps, label):
+    """`steps` eager decode steps of the GPU model and the oracle from the same ids, each step's logits within the
+    bf16 tolerance; the next ids are the oracle's greedy choice (so both caches see the same history)."""
+    for step in range(steps):
+        want = ref.logits(ids, rc)[:, -1]
+        got = gpu.logits(ids, gc)
+        gap = float(np.max(np.abs(got - want)))
+        say(f"  {label} step {step}: max|d| {gap:.3g} (max |logit| {np.max(np.abs(want)):.3g})")
+        assert gap <= 2e-2, (label, step)
+        ids = want.argmax(-1).reshape(-1, 1)
+    return ids

@@ -20,7 +20,7 @@ import pytest
 
 import ctorch_amd as ct
 import oracle
-from common import build_pair, rel_err
+from common import build_pair, greedy_steps, one_block_prefix, rel_err
 
 pytestmark = pytest.mark.gpu
 GPU = ct.device("gpu")
@@ -35,36 +35,6 @@ def say(msg):
 def _threads():
     oracle.lib()
     oracle.set_threads(16)
-
-
-def one_block_prefix(ref_cache, gpu_cache, layers, batch, kv_heads, length, head_dim, key, kv_dtype):
-    """The same seeded N(0, 1) K and V block (bf16-exact values) in every layer: appended to the GPU cache in its
-    dtype and written into the oracle's f32 cache."""
-    k = oracle.randn(oracle.fold_in(key, 0), batch * kv_heads * length * head_dim)
-    v = oracle.randn(oracle.fold_in(key, 1), batch * kv_heads * length * head_dim)
-    kb = oracle.bf16_encode(k).reshape(batch, kv_heads, length, head_dim)
-    vb = oracle.bf16_encode(v).reshape(batch, kv_heads, length, head_dim)
-    del k, v
-    kf, vf = oracle.bf16_decode(kb), oracle.bf16_decode(vb)
-    if kv_dtype == ct.BF16:
-        gk, gv = ct.Tensor.from_numpy(kb, ct.BF16, GPU), ct.Tensor.from_numpy(vb, ct.BF16, GPU)
-    else:
-        gk, gv = ct.Tensor.from_numpy(kf, ct.F32, GPU), ct.Tensor.from_numpy(vf, ct.F32, GPU)
-    for layer in range(layers):
-        # each layer gets its own copy of the block (an append copies into the layer's storage)
-        gpu_cache.append(layer, gk, gv)
-        ref_cache.fill(layer, length, kf, vf)
-
-
-def greedy_steps(ref, gpu, rc, gc, ids, steps, label):
-    for step in range(steps):
-        want = ref.logits(ids, rc)[:, -1]
-        got = gpu.logits(ids, gc)
-        gap = float(np.max(np.abs(got - want)))
-        say(f"  {label} step {step}: max|d| {gap:.3g} (max |logit| {np.max(np.abs(want)):.3g})")
-        assert gap <= 2e-2, (label, step)
-        ids = want.argmax(-1).reshape(-1, 1)
-    return ids
 
 
 # ------------------------------------------------------------------------------------------ C3

@@ -448,3 +448,18 @@ def test_lora_adapter_equals_merged_weight():
     assert np.max(np.abs(a - b)) < 1e-5
     base = oracle.OracleLM(plain_cfg, {k: v for k, v in w.items() if "_adapter" not in k})
     assert np.max(np.abs(a - base.logits(ids, base.make_cache(1)))) > 1e-3  # the adapter is not a no-op
+
+
+def test_last_logits_is_the_last_position_of_the_full_logits():
+    """OracleLM.last_logits runs the same C path as logits (embedding rows, orc_decoder_decode, orc_linear) with the
+    head restricted to each sequence's last row: the same bits as the last position of logits, for f32 and bf16
+    models, from an empty cache and from a cache that already holds a prefix."""
+    for dtype in ("f32", "bf16"):
+        cfg = oracle.ModelConfig(vocab=300, layers=2, dimensions=128, heads=4, kv_heads=2, hidden=256, context=40,
+                                 dtype=dtype, lora_rank=4 if dtype == "bf16" else 0, lora_alpha=8.0)
+        lm = oracle.OracleLM(cfg, oracle.synthesize_weights(cfg, (21, 0)))
+        ids = oracle.random_ids((22, 0), 3 * 17, cfg.vocab).reshape(3, 17)
+        a, b = lm.make_cache(3), lm.make_cache(3)
+        assert np.array_equal(lm.last_logits(ids[:, :9], a), lm.logits(ids[:, :9], b)[:, -1])
+        assert np.array_equal(lm.last_logits(ids[:, 9:], a), lm.logits(ids[:, 9:], b)[:, -1])
+        assert a.length == b.length == 17
