@@ -239,6 +239,8 @@ def cpu_baseline(threads=16):
       C1  the tiny f32 decoder in full: 32-byte prompt, then 128 greedy steps (1 thread);
       C2  1B bf16: the 128-token prompt (untimed setup, all threads), then 16 greedy decode steps timed (1 thread);
       C3  1B bf16 at batch 32 over a 2048-token seeded prefix: 2 decode steps timed (`threads` threads);
+      C4  8B-width: 8 decode steps of one layer at batch 8 over a 32768-position prefix, timed on `threads`
+          threads and reported for the 32-layer model as 32 x that time (embedding and LM head not timed);
       C5  1B bf16 + LoRA r16: a 1 x 512 prefill sample timed (`threads` threads).
     Weights are synthesised on the host with all threads before each leg (untimed)."""
     import oracle
@@ -301,6 +303,28 @@ def cpu_baseline(threads=16):
     legs["c3"] = dict(value=2 * B / sec, unit="tok/s", cores=threads, seconds=sec,
                       sample="C3: batch 32 over a 2048-token seeded prefix, 2 greedy decode steps (row-parallel)")
     del cache, lm3, lm
+    # C4: one layer of the 8B-width decoder (its weights only: a 16-entry vocabulary keeps the embedding and the
+    # head out of the way), 8 decode steps at batch 8 over a 32768-position prefix, each reported for the 32
+    # layers of the model.  The prefix holds constants, written to every page of the cache (the arithmetic's time does not depend
+    # on the values, and drawing 2 x 268M random values would cost a minute)
+    c4 = oracle.ModelConfig(vocab=16, layers=1, dimensions=4096, heads=32, kv_heads=8, hidden=14336,
+                            context=32768 + 16, dtype="bf16", rope_base=500000.0)
+    lm4 = lm_for(c4, (88, 0))
+    B4, P4 = 8, 32768
+    cache = lm4.make_cache(B4)
+    cache.keys[0][:, :, :P4] = 0.25
+    cache.values[0][:, :, :P4] = -0.5
+    cache.structs[0].length = P4
+    x4 = np.random.default_rng(12).standard_normal((B4, 1, c4.dimensions), dtype=np.float32)
+    def c4_steps():
+        for _ in range(8):
+            lm4.decode(x4, cache)
+    _, sec = timed(c4_steps, threads)
+    legs["c4"] = dict(value=8 * B4 / (32 * sec), unit="tok/s", cores=threads, seconds=sec, layers_timed=1,
+                      sample="C4: 8 decode steps of one 8B-width layer (d 4096, 32/8 heads, head dim 128, SwiGLU "
+                             "14336) at batch 8 over 32768-32775 cached positions, reported as 32 x the layer "
+                             "time (embedding and LM head not timed; row-parallel)")
+    del cache, lm4
     # C5
     c5 = oracle.ModelConfig(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632, context=520,
                             dtype="bf16", lora_rank=16, lora_alpha=32.0)
@@ -406,7 +430,7 @@ def main():
 
     baseline = None
     if not args.no_cpu_baseline:
-        log("bench: CPU oracle baseline (C1, C2 single thread; C3, C5 row-parallel samples)")
+        log("bench: CPU oracle baseline (C1, C2 single thread; C3, C4, C5 row-parallel samples)")
         baseline = cpu_baseline()
         log("bench: CPU " + ", ".join(f"{k} {v['value']:.3g} {v['unit']} ({v['cores']} thr, {v['seconds']:.1f} s)"
                                       for k, v in baseline["legs"].items()) + f" on {baseline['cpu_model']}")
