@@ -181,8 +181,8 @@ def test_operators_match_the_oracle():
         assert rel_err(y, oracle.linear(x, weight)) <= 1e-5
     # several rows over bf16 weights with 16-row tiles take the matrix cores: activations split into bf16
     # hi + lo (each product carries ~2^-17 relative error), so the bound is the f32 logit tolerance, 1e-4
-    # (runs of 1..4 staged chunks take the up-front variant: 3 of 4 at (3, 16, 768), 4 at (20, 96, 512), 2 at
-    # (3, 80, 512); longer runs the double-buffered loop, with an odd chunk count at (9, 80, 1792); at most four
+    # (runs of 1..2 staged chunks take the up-front variant: 2 at (3, 80, 512); longer runs the double-buffered
+    # loop: 3 chunks at (3, 16, 768), 4 at (20, 96, 512), an odd count at (9, 80, 1792); at most four
     # 16-row tiles over up to 32 rows and K a multiple of 512 take the few-tile kernel: (20, 32, 512), (3, 48, 1024),
     # (32, 64, 2048))
     for rows, n, k in ((5, 320, 2048), (37, 64, 512), (64, 48, 4096), (3, 16, 768), (20, 96, 512), (3, 80, 512),
