@@ -31,8 +31,12 @@ constexpr int kMaxRows = 64;                    // activation rows per launch
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-/// k per staged chunk: the double-buffered hi/lo rows stay within 64 KB of LDS.
-constexpr int chunk_k(int mt) { return mt == 1 ? 256 : mt == 2 ? 128 : 64; }
+/// k per staged chunk: the smallest the staging map takes (each row's 4-column groups span at most half a
+/// work-group).  Shorter chunks pipeline the loads finer against the staging and the products; measured on MI355X
+/// (1B widths, A/B on one box): 16 rows 256 -> 128 (gate/up at batch 32 in row parts 16.25 -> 15.55 us a layer,
+/// the batch-4 LoRA decode step 1.29 -> 1.24 ms), 32 rows 128 -> 64 (QKV at batch 32 7.35 -> 6.34 us a layer);
+/// 512 at 16 rows was slower (gate/up 19.0 us).
+constexpr int chunk_k(int mt) { return mt == 1 ? 128 : 64; }
 constexpr int lds_stride(int mt) { return chunk_k(mt) + 8; } // bf16 elements per staged row (bank spread)
 /// LDS of a work-group: NC staged chunks (two for the double-buffered loop, NC = 0) of hi and lo rows.
 constexpr size_t lds_bytes(int mt, int nc) { return size_t(nc > 2 ? nc : 2) * 2 * 16 * mt * lds_stride(mt) * 2; }
