@@ -5,14 +5,15 @@
 // l supplies A = W[row l%16][k 8*(l/16) .. +8] (16 contiguous bytes of a weight row, so the weights stream from
 // HBM in their row-major layout), B = X[row l%16][k 8*(l/16) .. +8], and receives D[rows 4*(l/16) .. +4][l%16].
 //
-// A work-group is four waves; each wave owns one tile of 16 weight rows and all activation rows (MT tiles of
+// A work-group is eight waves; each wave owns one tile of 16 weight rows and all activation rows (MT tiles of
 // 16).  The activation rows are staged per K-chunk in LDS as bf16 pairs hi + lo (x = hi + lo to ~2^-16), so every
 // product is two MFMAs and the result keeps f32-level accuracy against a bf16 weight.  The RMSNorm of the
 // activation rows is fused: the staged rows are x * g, the sums of squares accumulate while staging, and the
 // per-row factor 1/sqrt(mean x^2 + eps) scales the finished dot products.  A work-group of up to two chunks
 // (NC = 2) issues every activation and weight load of its chunks at once, stages them all, and computes: one
-// memory round trip.  Longer runs (NC = 0) double buffer the chunks in LDS, loading the next chunk's activations
-// (into registers) and weights while the current chunk is used.
+// memory round trip.  Longer runs double buffer the chunks in LDS: with repacked weights and a run of 4, 8, 16 or
+// 32 chunks (NC = the run) the weights of the next three chunks are in flight while one is used; otherwise
+// (NC = 0) the next chunk's activations (into registers) and weights.
 //
 // Tile rows: generic epilogues take 16 consecutive rows of one weight segment; SwiGLU interleaves gate and up
 // (tile row 2j = gate row 8T + j, 2j + 1 = up row 8T + j), so every lane holds (gate, up) pairs and QKV holds
@@ -38,12 +39,20 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 /// 512 at 16 rows was slower (gate/up 19.0 us).
 constexpr int chunk_k(int mt) { return mt == 1 ? 128 : 64; }
 constexpr int lds_stride(int mt) { return chunk_k(mt) + 8; } // bf16 elements per staged row (bank spread)
-/// LDS of a work-group: NC staged chunks (two for the double-buffered loop, NC = 0) of hi and lo rows.
-constexpr size_t lds_bytes(int mt, int nc) { return size_t(nc > 2 ? nc : 2) * 2 * 16 * mt * lds_stride(mt) * 2; }
-/// Up-front variant for a run of `nchunks` chunks: 2 (that many chunks at most), or 0 for the loop.  Runs of three
-/// or four chunks take the loop: measured on MI355X at batch 32 (1B, down projection in 11 key slices of 4 chunks)
-/// 11.2 us a layer against 12.7 with all four chunks' loads up front (C3 step 1.242 -> 1.224 ms).
-constexpr int upfront_chunks(int nchunks) { return nchunks <= 2 ? 2 : 0; }
+/// LDS of a work-group: two staged chunks of hi and lo rows (every variant).
+constexpr size_t lds_bytes(int mt) { return size_t(2) * 2 * 16 * mt * lds_stride(mt) * 2; }
+/// Variant for a run of `nchunks` chunks: 2 (all loads up front; that many chunks at most), the run length itself
+/// (the deep pipeline, unrolled over a run of 4, 8, 16 or 32 chunks; `deep`: repacked weights and 16 or more
+/// activation rows per work-group), or 0 for the double-buffered loop.  Measured on MI355X (A/B, one box): at batch
+/// 32 (1B) the deep pipeline took the C3 step 1.190-1.204 -> 1.168-1.170 ms (gate/up 15.5 -> 14.9 us, down 11.7-12.2
+/// -> 10.9, LM head 30.5-31.1 -> 29.3); at 8 rows (8B, batch 8) the QKV and gate/up launches, already streaming at
+/// ~5.6 TB/s, lost 1-1.7 us each, so those keep the loop.  Runs of three or four chunks take a loop, not all loads
+/// up front (C3 down projection in 11 key slices of 4 chunks: 11.2 us a layer against 12.7).
+constexpr int loop_variant(int nchunks, bool deep) {
+    if (nchunks <= 2) return 2;
+    if (deep && (nchunks == 4 || nchunks == 8 || nchunks == 16 || nchunks == 32)) return nchunks;
+    return 0;
+}
 /// Most key slices a launch takes (the reduce kernel keeps them all in flight).
 constexpr int kMaxSplits = 16;
 
@@ -53,6 +62,14 @@ inline bool eligible(const dlk_gemv_params& p) {
     if (p.epilogue == DLK_EPI_SWIGLU) return p.seg_rows[0] % 8 == 0;
     for (int s = 0; s < p.nseg; ++s)
         if (p.seg_rows[s] % kTile != 0) return false;
+    return true;
+}
+
+/// Whether every weight segment of the launch comes repacked in tile order (w_tiles).
+inline bool repacked(const dlk_gemv_params& p) {
+    const int segs = p.epilogue == DLK_EPI_SWIGLU ? 1 : p.nseg;
+    for (int s = 0; s < segs; ++s)
+        if (!p.w_tiles[s]) return false;
     return true;
 }
 
@@ -358,7 +375,16 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params laun
     for (int i = 0; i < XR; ++i) squares[i] = 0.0f;
     auto stage = [&](int buf, const float4 (&xr)[XR], const u32x4& graw) {
         float g[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-        if constexpr (NORM) {
+        if constexpr (NORM && NC >= 4) {
+            // selects, not branches: a load used only inside a branch is sunk into it by the compiler, issued
+            // after the loads that follow it in the source, and its wait then drains those too (the deep
+            // pipeline's prologue; the other variants measured faster with the branches)
+            const float gb[4] = {bf16_lo(graw.x), bf16_hi(graw.x), bf16_lo(graw.y), bf16_hi(graw.y)};
+            const float gf[4] = {__uint_as_float(graw.x), __uint_as_float(graw.y), __uint_as_float(graw.z),
+                                 __uint_as_float(graw.w)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) g[i] = affine ? (p.norm_bf16 ? gb[i] : gf[i]) : 1.0f;
+        } else if constexpr (NORM) {
             if (affine) {
                 if (p.norm_bf16) {
                     g[0] = bf16_lo(graw.x); g[1] = bf16_hi(graw.x); g[2] = bf16_lo(graw.y); g[3] = bf16_hi(graw.y);
@@ -424,7 +450,40 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params laun
         }
     };
 
-    if constexpr (NC > 0) {
+    if constexpr (NC >= 4) {
+        // Deep pipeline over a run of exactly NC chunks (the launch reads repacked weights): at step c the loads
+        // of chunk c + 3 are issued first, so the weights of c + 1 .. c + 3 stay in flight while chunk c is used;
+        // a chunk's activations are issued before its weights, so waiting for the ones staged next leaves the
+        // later weights in flight.  Four register sets rotate with the steps; the run is unrolled whole, so every
+        // wait counts exactly the loads issued after the one it needs.
+        float4 xs[4][XR];
+        u32x4 gs[4], ws[4][STEPS];
+        // the first three chunks' activations, then their weights chunk by chunk, in that order (scheduling
+        // barriers keep the compiler from interleaving them): the wait for chunk 0's activations leaves every
+        // weight load in flight, and the one for chunk 0's weights those of chunks 1 and 2
+#pragma unroll
+        for (int c = 0; c < 3; ++c) load_x(c, xs[c], gs[c]);
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_w(c, ws[c]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        stage(0, xs[0], gs[0]);
+        gemv::lds_barrier();
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (c + 3 < NC) {
+                load_x(c + 3, xs[(c + 3) % 4], gs[(c + 3) % 4]);
+                load_w(c + 3, ws[(c + 3) % 4]);
+            }
+            compute(c % 2, ws[c % 4]);
+            if (c + 1 < NC) {
+                stage((c + 1) % 2, xs[(c + 1) % 4], gs[(c + 1) % 4]);
+                gemv::lds_barrier();
+            }
+        }
+    } else if constexpr (NC == 2) {
         // every load of the run first (chunks past the run repeat its last chunk: loads stay unconditional, so
         // no branch drains them early), then the staging of the run's chunks into NC buffers and the products
         float4 xs[NC][XR];
@@ -822,7 +881,7 @@ gemv::Kernel resolve_reduce(const dlk_gemv_params& p) {
     }
 }
 
-/// The matrix-core kernel for mt (1, 2 or 4) activation tiles and nc (upfront_chunks) chunks, or the few-tile
+/// The matrix-core kernel for mt (1, 2 or 4) activation tiles and loop variant nc (loop_variant), or the few-tile
 /// kernel (nc = -1, mt 1 or 2); {} if none.
 template <int EPI>
 gemv::Kernel resolve(const dlk_gemv_params& p, int mt, int nc) {
@@ -835,14 +894,23 @@ gemv::Kernel resolve(const dlk_gemv_params& p, int mt, int nc) {
                 return {};
             }
         }
-#define DLK_GEMM_ROWS(MT, NC) {reinterpret_cast<const void*>(&gemm_rows<EPI, N, MT, NC>), lds_bytes(MT, NC)}
-        switch (mt * 8 + nc) {
-        case 8: return DLK_GEMM_ROWS(1, 0);
-        case 10: return DLK_GEMM_ROWS(1, 2);
-        case 16: return DLK_GEMM_ROWS(2, 0);
-        case 18: return DLK_GEMM_ROWS(2, 2);
-        case 32: return DLK_GEMM_ROWS(4, 0);
-        case 34: return DLK_GEMM_ROWS(4, 2);
+#define DLK_GEMM_ROWS(MT, NC) {reinterpret_cast<const void*>(&gemm_rows<EPI, N, MT, NC>), lds_bytes(MT)}
+        auto by_run = [&](auto mtc) -> gemv::Kernel {
+            constexpr int MT = decltype(mtc)::value;
+            switch (nc) {
+            case 0: return DLK_GEMM_ROWS(MT, 0);
+            case 2: return DLK_GEMM_ROWS(MT, 2);
+            case 4: return DLK_GEMM_ROWS(MT, 4);
+            case 8: return DLK_GEMM_ROWS(MT, 8);
+            case 16: return DLK_GEMM_ROWS(MT, 16);
+            case 32: return DLK_GEMM_ROWS(MT, 32);
+            default: return {};
+            }
+        };
+        switch (mt) {
+        case 1: return by_run(std::integral_constant<int, 1>{});
+        case 2: return by_run(std::integral_constant<int, 2>{});
+        case 4: return by_run(std::integral_constant<int, 4>{});
         default: return {};
         }
 #undef DLK_GEMM_ROWS

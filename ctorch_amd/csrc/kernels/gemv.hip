@@ -121,7 +121,8 @@ int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
         const int parts = (p.M + 15) / 16;
         if (p.epilogue == DLK_EPI_SWIGLU && parts > 1 && blocks >= 64 && blocks * parts <= 256 && blocks % 8 == 0) {
             p.row_parts = parts;
-            const Kernel kernel = resolve_gemm(p, 1, upfront_chunks(p.K / chunk_k(1)));
+            // parts of 16 rows: the deep pipeline when the weights come repacked
+            const Kernel kernel = resolve_gemm(p, 1, loop_variant(p.K / chunk_k(1), repacked(p)));
             if (!kernel.fn) return static_cast<int>(hipErrorInvalidValue);
             void* args[] = {&p};
             const hipError_t status =
@@ -139,7 +140,8 @@ int launch_gemm(const dlk_gemv_params& params, hipStream_t stream) {
         if (p.defer_reduce && (splits == 1 || p.epilogue != DLK_EPI_QKV || params.M > kMaxRows))
             return static_cast<int>(hipErrorInvalidValue);
         const int mt = row_tiles(p.M);
-        const Kernel kernel = resolve_gemm(p, mt, upfront_chunks(p.K / splits / chunk_k(mt)));
+        const bool deep = repacked(p) && p.M >= 16;
+        const Kernel kernel = resolve_gemm(p, mt, loop_variant(p.K / splits / chunk_k(mt), deep));
         if (!kernel.fn) return static_cast<int>(hipErrorInvalidValue);
         const int64_t* bump = p.bump_position;
         if (splits > 1) p.bump_position = nullptr; // the reduce launch advances the length
