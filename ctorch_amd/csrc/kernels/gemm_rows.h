@@ -41,6 +41,9 @@ constexpr int chunk_k(int mt) { return mt == 1 ? 128 : 64; }
 constexpr int lds_stride(int mt) { return chunk_k(mt) + 8; } // bf16 elements per staged row (bank spread)
 /// LDS of a work-group: two staged chunks of hi and lo rows (every variant).
 constexpr size_t lds_bytes(int mt) { return size_t(2) * 2 * 16 * mt * lds_stride(mt) * 2; }
+/// Chunks the deep pipeline keeps in flight ahead of the one in use.  Measured on MI355X (C3 step, A/B on one box):
+/// 3 ahead 1.183 ms; 4 (16-row tiles) / 6 (32-row tiles) ahead 1.198-1.210 ms; 5 / 8 ahead 1.214-1.225 ms.
+constexpr int kDeepAhead = 3;
 /// Variant for a run of `nchunks` chunks: 2 (all loads up front; that many chunks at most), the run length itself
 /// (the deep pipeline, unrolled over a run of 4, 8, 16 or 32 chunks; `deep`: repacked weights and 16 or more
 /// activation rows per work-group), or 0 for the double-buffered loop.  Measured on MI355X (A/B, one box): at batch
@@ -452,19 +455,20 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params laun
 
     if constexpr (NC >= 4) {
         // Deep pipeline over a run of exactly NC chunks (the launch reads repacked weights): at step c the loads
-        // of chunk c + 3 are issued first, so the weights of c + 1 .. c + 3 stay in flight while chunk c is used;
-        // a chunk's activations are issued before its weights, so waiting for the ones staged next leaves the
-        // later weights in flight.  Four register sets rotate with the steps; the run is unrolled whole, so every
-        // wait counts exactly the loads issued after the one it needs.
-        float4 xs[4][XR];
-        u32x4 gs[4], ws[4][STEPS];
-        // the first three chunks' activations, then their weights chunk by chunk, in that order (scheduling
-        // barriers keep the compiler from interleaving them): the wait for chunk 0's activations leaves every
-        // weight load in flight, and the one for chunk 0's weights those of chunks 1 and 2
+        // of chunk c + A (A = kDeepAhead) are issued first, so the weights of c + 1 .. c + A stay in flight while
+        // chunk c is used; a chunk's activations are issued before its weights, so waiting for the ones staged
+        // next leaves the later weights in flight.  A + 1 register sets rotate with the steps; the run is unrolled
+        // whole, so every wait counts exactly the loads issued after the one it needs.
+        constexpr int A = kDeepAhead, SETS = A + 1, PRE = A < NC ? A : NC;
+        float4 xs[SETS][XR];
+        u32x4 gs[SETS], ws[SETS][STEPS];
+        // the first chunks' activations, then their weights chunk by chunk, in that order (scheduling barriers
+        // keep the compiler from interleaving them): the wait for chunk 0's activations leaves every weight load
+        // in flight, and the one for chunk 0's weights those of the later chunks
 #pragma unroll
-        for (int c = 0; c < 3; ++c) load_x(c, xs[c], gs[c]);
+        for (int c = 0; c < PRE; ++c) load_x(c, xs[c], gs[c]);
 #pragma unroll
-        for (int c = 0; c < 3; ++c) {
+        for (int c = 0; c < PRE; ++c) {
             __builtin_amdgcn_sched_barrier(0);
             load_w(c, ws[c]);
         }
@@ -473,13 +477,13 @@ __global__ __launch_bounds__(kThreads) void gemm_rows(const dlk_gemv_params laun
         gemv::lds_barrier();
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            if (c + 3 < NC) {
-                load_x(c + 3, xs[(c + 3) % 4], gs[(c + 3) % 4]);
-                load_w(c + 3, ws[(c + 3) % 4]);
+            if (c + A < NC) {
+                load_x(c + A, xs[(c + A) % SETS], gs[(c + A) % SETS]);
+                load_w(c + A, ws[(c + A) % SETS]);
             }
-            compute(c % 2, ws[c % 4]);
+            compute(c % 2, ws[c % SETS]);
             if (c + 1 < NC) {
-                stage((c + 1) % 2, xs[(c + 1) % 4], gs[(c + 1) % 4]);
+                stage((c + 1) % 2, xs[(c + 1) % SETS], gs[(c + 1) % SETS]);
                 gemv::lds_barrier();
             }
         }
