@@ -94,33 +94,11 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
     const int bk = blockIdx.y;
     const int b = bk / p.KV, kvh = bk % p.KV;
     const int G = p.H / p.KV;
-    const int64_t S = (p.position ? *p.position : p.first_host) + 1;
-    const int active = static_cast<int>((S + p.chunk - 1) / p.chunk);
-    if (split >= active) {
-        // no keys here: the combine pass gives this slot zero weight
-        if (t < G) {
-            const int64_t slot = (static_cast<int64_t>(b) * p.H + kvh * G + t) * p.splits + split;
-            p.partial_ml[slot * 2] = -INFINITY;
-            p.partial_ml[slot * 2 + 1] = 0.0f;
-        }
-        return;
-    }
     const int per_wave = p.chunk / W;
-    const int64_t k_end = min(S, static_cast<int64_t>(split) * p.chunk + p.chunk);
     const int64_t w_begin = static_cast<int64_t>(split) * p.chunk + static_cast<int64_t>(wave) * per_wave;
-    const int keys = static_cast<int>(max<int64_t>(0, min<int64_t>(k_end, w_begin + per_wave) - w_begin));
-    const int tiles = (keys + kTileKeys - 1) / kTileKeys;
-
-    // the query heads of this KV head as the B operand (column col = head kvh G + col), scaled into base 2; set
-    // below, after the first K/V tile is requested
-    bf16x8 qh[KS], ql[KS];
-
-    // buffer ranges over this wave's keys: rows past them read as zero
     const size_t head = (static_cast<size_t>(b) * p.KV + kvh) * p.capacity + w_begin;
-    const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<KT*>(static_cast<const KT*>(p.k) + head * HD), 0, keys * ROW, kBufferFlags);
-    const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<KT*>(static_cast<const KT*>(p.v) + head * HD), 0, keys * ROW, kBufferFlags);
+    KT* const k_base = const_cast<KT*>(static_cast<const KT*>(p.k) + head * HD);
+    KT* const v_base = const_cast<KT*>(static_cast<const KT*>(p.v) + head * HD);
     // K fragment (half u, k step st): key 16 u + col, head dims 32 st + 8 q .. +8.  V: key pair kp = col (keys
     // 2 kp, 2 kp + 1), pieces dg = q + 4 i.
     const int k_offset = col * ROW + (8 * q) * static_cast<int>(sizeof(KT));
@@ -129,7 +107,7 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
         u32x4 k[2][KS][KL];
         u32x4 v[VI][2];
     };
-    auto load = [&](int tile, Tile& dst) {
+    auto load = [&](int tile, Tile& dst, __amdgpu_buffer_rsrc_t kres, __amdgpu_buffer_rsrc_t vres) {
         const int base = tile * kTileKeys * ROW;
 #pragma unroll
         for (int u = 0; u < 2; ++u)
@@ -146,6 +124,61 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
                 dst.v[i][e] = __builtin_amdgcn_raw_buffer_load_b128(vres, base + v_offset + e * ROW + 64 * i, 0, 0);
     };
 
+    // Four-wave work-groups (long runs of keys: batched decode, key splits) request the first tile and (without
+    // the QKV partials) the query rows before the device length arrives: the first tile's range is the wave's run
+    // within the cache capacity, so its rows past the length hold whatever the cache held (their scores are
+    // masked, their values zeroed in use()).  Later tiles read through ranges that end at the length.  Measured on
+    // MI355X (A/B, one box): C3 1.181 -> 1.163 ms a step, C4 9.34-9.39 -> 9.29-9.33 ms; the eight-wave
+    // one-sequence launch (C2, short runs, several waves without keys) went 550 -> 571 us a step that way, so it
+    // reads the length first.
+    constexpr bool EARLY = W == 4;
+    Tile a, c;
+    float4 xq[KS][2];
+    auto load_q = [&]() {
+        if constexpr (!FINISH) {
+            const float* qrow =
+                p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G + min(col, G - 1)) * HD;
+#pragma unroll
+            for (int st = 0; st < KS; ++st) {
+                xq[st][0] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q);
+                xq[st][1] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q + 4);
+            }
+        }
+    };
+    if constexpr (EARLY) {
+        const int room = static_cast<int>(max<int64_t>(0, min<int64_t>(per_wave, p.capacity - w_begin)));
+        load_q();
+        load(0, a, __builtin_amdgcn_make_buffer_rsrc(k_base, 0, room * ROW, kBufferFlags),
+             __builtin_amdgcn_make_buffer_rsrc(v_base, 0, room * ROW, kBufferFlags));
+    }
+
+    const int64_t S = (p.position ? *p.position : p.first_host) + 1;
+    const int active = static_cast<int>((S + p.chunk - 1) / p.chunk);
+    if (split >= active) {
+        // no keys here: the combine pass gives this slot zero weight
+        if (t < G) {
+            const int64_t slot = (static_cast<int64_t>(b) * p.H + kvh * G + t) * p.splits + split;
+            p.partial_ml[slot * 2] = -INFINITY;
+            p.partial_ml[slot * 2 + 1] = 0.0f;
+        }
+        return;
+    }
+    const int64_t k_end = min(S, static_cast<int64_t>(split) * p.chunk + p.chunk);
+    const int keys = static_cast<int>(max<int64_t>(0, min<int64_t>(k_end, w_begin + per_wave) - w_begin));
+    const int tiles = (keys + kTileKeys - 1) / kTileKeys;
+
+    // buffer ranges over this wave's keys: rows past them read as zero
+    const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(k_base, 0, keys * ROW, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(v_base, 0, keys * ROW, kBufferFlags);
+    if constexpr (!EARLY) {
+        // the query loads first, then the first tile's (the query split waits for the query rows only)
+        load_q();
+        if (tiles > 0) load(0, a, kres, vres);
+    }
+
+    // the query heads of this KV head as the B operand (column col = head kvh G + col), scaled into base 2
+    bf16x8 qh[KS], ql[KS];
+
     f32x4 o[DT], l = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < DT; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -154,10 +187,15 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
     uint16_t* my_vt = &vt[wave][0][0];
 
     auto use = [&](int tile, const Tile& cur) {
+        // values of keys past the wave's run (the first tile of an early request only: its range did not wait
+        // for the length) are zeroed, so that their zero probabilities cannot meet a non-finite value
+        const bool cut = EARLY && tile == 0 && keys < kTileKeys;
+        const bool live0 = !cut || 2 * col < keys, live1 = !cut || 2 * col + 1 < keys;
         // V^T of the tile into the wave's LDS tile (word = key pair kp of one head-dim row)
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            const u32x4 a = cur.v[i][0], c = cur.v[i][1];
+            const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+            const u32x4 a = live0 ? cur.v[i][0] : zero, c = live1 ? cur.v[i][1] : zero;
             if constexpr (F32) {
                 // piece dg = q + 4 i holds head dims 4 dg .. +4 of keys 2 kp (a) and 2 kp + 1 (c)
                 u32x2 h0, l0, h1, l1;
@@ -263,7 +301,6 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
     const bool holder = finish && split == active - 1 && newest >= w_begin && newest < w_begin + keys;
     const int patch_tile = holder ? static_cast<int>(newest - w_begin) / kTileKeys : -1;
     const int patch_key = holder ? static_cast<int>(newest - w_begin) % kTileKeys : 0;
-    Tile a, c;
     {
         const float qs = p.scale * 1.4426950408889634f;
         const float z = col < G ? qs : 0.0f;
@@ -278,7 +315,6 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
             }
         };
         if constexpr (finish) {
-            if (tiles > 0) load(0, a);
             constexpr int kBatch = 8; // slices requested at once
             constexpr int UNITS = HD / 4; // 4-dim units per head row
             const int width = p.qkv_width;
@@ -367,20 +403,11 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
             split_q(stage + min(col, G - 1) * HD);
             __asm__ volatile("" ::: "memory");
         } else {
-            // the query loads first, then the first tile's, then the split (which waits for the query rows only)
-            const float* qrow =
-                p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G + min(col, G - 1)) * HD;
-            float4 x[KS][2];
-#pragma unroll
-            for (int st = 0; st < KS; ++st) {
-                x[st][0] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q);
-                x[st][1] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q + 4);
-            }
-            if (tiles > 0) load(0, a);
+            // the query rows were requested before the first tile, so this split waits for them only
 #pragma unroll
             for (int st = 0; st < KS; ++st)
-                split8(f32x8{x[st][0].x, x[st][0].y, x[st][0].z, x[st][0].w, x[st][1].x, x[st][1].y, x[st][1].z,
-                             x[st][1].w} * z, qh[st], ql[st]);
+                split8(f32x8{xq[st][0].x, xq[st][0].y, xq[st][0].z, xq[st][0].w, xq[st][1].x, xq[st][1].y,
+                             xq[st][1].z, xq[st][1].w} * z, qh[st], ql[st]);
         }
     }
     // The holder's new key in its tile's registers (K: lanes col = key % 16 of half key / 16 hold dims
@@ -425,11 +452,11 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
         int tile = 0;
         for (;;) {
             if (tile + 1 >= tiles) { patch(tile, a); use(tile, a); break; }
-            load(tile + 1, c);
+            load(tile + 1, c, kres, vres);
             use(tile, a);
             ++tile;
             if (tile + 1 >= tiles) { patch(tile, c); use(tile, c); break; }
-            load(tile + 1, a);
+            load(tile + 1, a, kres, vres);
             use(tile, c);
             ++tile;
         }
