@@ -385,6 +385,47 @@ def test_decode_over_split_keys_merges_partials(kv):
 
 
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
+@pytest.mark.parametrize("batch", [2, 4])
+def test_cache_rows_past_the_length_never_reach_the_decode(batch, kv):
+    # The key-split decode attention requests each wave's first K/V tile before it reads the device length, so
+    # the tile holds the cache rows past the length.  Those rows are filled with NaN here (appended, then the
+    # cache truncated back); with a 1024-token prefix a wave's run starts at the new position, so its first tile
+    # is the new key and 31 NaN rows.  Batch 2 projects QKV on the vector path, batch 4 in key slices that the
+    # attention finishes.
+    say(f"case: B={batch} decode over a 1024-token {kv} prefix with NaN cache rows past the length")
+    cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=512, context=1100,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(44, 0), scale=0.05, kv_dtype=KV_DTYPES[kv])
+    B, P, hd, stale = batch, 1024, cfg.head_dim, 40
+    rc, gc = ref.make_cache(B), gpu.cache()
+    dev = ct.device("gpu")
+    if KV_DTYPES[kv] == ct.BF16:
+        nan = ct.Tensor.from_numpy(np.full((B, 2, stale, hd), 0x7FC0, np.uint16), ct.BF16, dev)
+    else:
+        nan = ct.Tensor.from_numpy(np.full((B, 2, stale, hd), np.nan, np.float32), ct.F32, dev)
+    for layer in range(cfg.layers):
+        k = oracle.randn(oracle.fold_in((85, 0), 2 * layer), B * 2 * P * hd).reshape(B, 2, P, hd)
+        v = oracle.randn(oracle.fold_in((85, 0), 2 * layer + 1), B * 2 * P * hd).reshape(B, 2, P, hd)
+        seed_prefix(rc, gc, layer, k, v, KV_DTYPES[kv])
+        gc.append(layer, nan, nan)
+    gc.truncate(P)
+    ids = oracle.random_ids((86, 0), B, cfg.vocab).reshape(B, 1)
+    steps = 8
+    tokens, last = gpu.generate(ids, steps, 0.0, (0, 0), use_graph=False, cache=gc)
+    assert np.all(np.isfinite(last))
+    history = np.concatenate([ids, tokens[:, :-1]], 1)
+    want = ref.logits(history, rc)
+    assert np.max(np.abs(last - want[:, -1])) <= 2e-2
+    for b in range(B):
+        for step in range(steps):
+            assert want[b, step, tokens[b, step]] >= want[b, step].max() - 4e-2, (b, step)
+    # the graph-replayed loop over the same request (rows P + 8 .. P + 39 still NaN) gives the same bits
+    gc.truncate(P)
+    graph_tokens, graph_last = gpu.generate(ids, steps, 0.0, (0, 0), use_graph=True, cache=gc)
+    assert np.array_equal(graph_tokens, tokens) and np.array_equal(graph_last, last)
+
+
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
 @pytest.mark.parametrize("dimensions,heads,kv_heads", [(512, 8, 2), (512, 8, 4), (512, 8, 8), (1024, 8, 2)])
 def test_streaming_decode_attention_over_many_keys(dimensions, heads, kv_heads, kv):
     # B * KV * prefix >= 32768 keys in all: one-position steps give each wave of the matrix-core kernel its own
