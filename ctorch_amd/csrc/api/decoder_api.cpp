@@ -118,6 +118,7 @@ dl_status dl_grouped_query_attention_noalloc(const float* query, const void* key
         p.v = value;
         p.capacity = source;
         p.first_host = source - length;
+        p.early_keys = source;
         p.B = static_cast<int>(batch); p.L = static_cast<int>(length); p.H = static_cast<int>(heads);
         p.KV = static_cast<int>(kv_heads); p.hd = static_cast<int>(D);
         p.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));

@@ -124,30 +124,29 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
                 dst.v[i][e] = __builtin_amdgcn_raw_buffer_load_b128(vres, base + v_offset + e * ROW + 64 * i, 0, 0);
     };
 
-    // Four-wave work-groups (long runs of keys: batched decode, key splits) request the first tile and (without
-    // the QKV partials) the query rows before the device length arrives: the first tile's range is the wave's run
+    // A wave whose run starts below the caller's early_keys requests its first tile (after the query rows, when
+    // no QKV partials are to be summed) before the device length arrives: that tile's range is the wave's run
     // within the cache capacity, so its rows past the length hold whatever the cache held (their scores are
-    // masked, their values zeroed in use()).  Later tiles read through ranges that end at the length.  Measured on
-    // MI355X (A/B, one box): C3 1.181 -> 1.163 ms a step, C4 9.34-9.39 -> 9.29-9.33 ms; the eight-wave
-    // one-sequence launch (C2, short runs, several waves without keys) went 550 -> 571 us a step that way, so it
-    // reads the length first.
-    constexpr bool EARLY = W == 4;
+    // masked, their values zeroed in use()).  The other waves, and every later tile, read through ranges that end
+    // at the length.  Measured on MI355X (A/B, one box), with every wave of four-wave work-groups requesting
+    // early: C3 1.181 -> 1.163 ms a step, C4 9.34-9.39 -> 9.29-9.33 ms; with every wave of the one-sequence launch
+    // too (C2: eight waves, most past the length) C2 went 550 -> 571 us, which the hint avoids (waves past the
+    // known keys fetched cache rows no step had touched).  With the hint: C3 1.176 -> 1.162 ms, C2, C4 and the
+    // C5 decode unchanged.
+    const bool early = w_begin < p.early_keys;
     Tile a, c;
     float4 xq[KS][2];
-    auto load_q = [&]() {
-        if constexpr (!FINISH) {
-            const float* qrow =
-                p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G + min(col, G - 1)) * HD;
+    if constexpr (!FINISH) {
+        const float* qrow =
+            p.q + static_cast<int64_t>(b) * p.ldq + static_cast<int64_t>(kvh * G + min(col, G - 1)) * HD;
 #pragma unroll
-            for (int st = 0; st < KS; ++st) {
-                xq[st][0] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q);
-                xq[st][1] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q + 4);
-            }
+        for (int st = 0; st < KS; ++st) {
+            xq[st][0] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q);
+            xq[st][1] = *reinterpret_cast<const float4*>(qrow + 32 * st + 8 * q + 4);
         }
-    };
-    if constexpr (EARLY) {
+    }
+    if (early) {
         const int room = static_cast<int>(max<int64_t>(0, min<int64_t>(per_wave, p.capacity - w_begin)));
-        load_q();
         load(0, a, __builtin_amdgcn_make_buffer_rsrc(k_base, 0, room * ROW, kBufferFlags),
              __builtin_amdgcn_make_buffer_rsrc(v_base, 0, room * ROW, kBufferFlags));
     }
@@ -170,11 +169,7 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
     // buffer ranges over this wave's keys: rows past them read as zero
     const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(k_base, 0, keys * ROW, kBufferFlags);
     const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(v_base, 0, keys * ROW, kBufferFlags);
-    if constexpr (!EARLY) {
-        // the query loads first, then the first tile's (the query split waits for the query rows only)
-        load_q();
-        if (tiles > 0) load(0, a, kres, vres);
-    }
+    if (!early && tiles > 0) load(0, a, kres, vres);
 
     // the query heads of this KV head as the B operand (column col = head kvh G + col), scaled into base 2
     bf16x8 qh[KS], ql[KS];
@@ -189,7 +184,7 @@ __global__ __launch_bounds__(W * kWave) void attention_matrix(const dlk_attentio
     auto use = [&](int tile, const Tile& cur) {
         // values of keys past the wave's run (the first tile of an early request only: its range did not wait
         // for the length) are zeroed, so that their zero probabilities cannot meet a non-finite value
-        const bool cut = EARLY && tile == 0 && keys < kTileKeys;
+        const bool cut = early && tile == 0 && keys < kTileKeys;
         const bool live0 = !cut || 2 * col < keys, live1 = !cut || 2 * col + 1 < keys;
         // V^T of the tile into the wave's LDS tile (word = key pair kp of one head-dim row)
 #pragma unroll

@@ -176,6 +176,11 @@ typedef struct dlk_attention_params {
        prefill kernels). */
     const unsigned char* keep_mask;
     int64_t mask_stride[4];
+    /* Matrix-core decode kernel: keys the caller knows the cache holds at this launch (its host length plus the
+       new position: the capture-time count for a replayed graph, whose length only grows), or 0.  A wave whose run
+       of keys starts below it requests its first K/V tile before it reads the device length.  A hint for speed
+       only: any value gives the same result. */
+    int64_t early_keys;
 } dlk_attention_params;
 
 /* Keys per split of a short one-position decode over a bf16 cache (few keys in all): 256 or 512, one work-group. */

@@ -239,6 +239,8 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         a.kv_bf16 = kv_bf16;
         a.capacity = cache.capacity();
         a.position = cache.position_data();
+        // the host length plus this chunk: at graph capture, the fewest keys any replay sees
+        a.early_keys = cache.length() + length;
         a.B = static_cast<int>(batch); a.L = static_cast<int>(length); a.H = static_cast<int>(H);
         a.KV = static_cast<int>(KV); a.hd = static_cast<int>(hd);
         a.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(hd)));

@@ -258,6 +258,7 @@ Tensor GroupedQueryAttention::run(const Tensor& input, KVCache* cache) {
     a.kv_bf16 = p.cache_bf16;
     a.capacity = target.capacity();
     a.position = target.position_data();
+    a.early_keys = offset + L; // the host length plus this chunk
     a.B = static_cast<int>(B); a.L = static_cast<int>(L); a.H = static_cast<int>(heads_); a.KV = static_cast<int>(kv_heads_);
     a.hd = static_cast<int>(hd);
     a.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(hd)));

@@ -232,6 +232,7 @@ Tensor grouped_query_attention(const Tensor& query, const Tensor& key, const Ten
     p.kv_bf16 = kv_dtype == DType::bf16;
     p.capacity = S;
     p.first_host = S - L; // unused: no causal window without a mask
+    p.early_keys = S;
     p.B = static_cast<int>(B); p.L = static_cast<int>(L); p.H = static_cast<int>(H); p.KV = static_cast<int>(KV);
     p.hd = static_cast<int>(D);
     p.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(D)));
