@@ -385,18 +385,19 @@ def test_decode_over_split_keys_merges_partials(kv):
 
 
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
-@pytest.mark.parametrize("batch", [2, 4])
-def test_cache_rows_past_the_length_never_reach_the_decode(batch, kv):
-    # The key-split decode attention requests each wave's first K/V tile before it reads the device length, so
-    # the tile holds the cache rows past the length.  Those rows are filled with NaN here (appended, then the
-    # cache truncated back); with a 1024-token prefix a wave's run starts at the new position, so its first tile
-    # is the new key and 31 NaN rows.  Batch 2 projects QKV on the vector path, batch 4 in key slices that the
-    # attention finishes.
-    say(f"case: B={batch} decode over a 1024-token {kv} prefix with NaN cache rows past the length")
-    cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=512, context=1100,
+@pytest.mark.parametrize("batch,prefix", [(2, 1024), (4, 1024), (4, 1064)])
+def test_cache_rows_past_the_length_never_reach_the_decode(batch, prefix, kv):
+    # The key-split decode attention requests a wave's first K/V tile before it reads the device length, so the
+    # tile holds the cache rows past the length.  Those rows are filled with NaN here (appended, then the cache
+    # truncated back).  With a 1024-token prefix a wave's run starts at the new position, so its first tile is the
+    # new key and 31 NaN rows; with 1064 that wave's second tile, read through a range that ends at the length,
+    # holds 9 live keys.  Batch 2 projects QKV on the vector path, batch 4 in key slices that the attention
+    # finishes.
+    say(f"case: B={batch} decode over a {prefix}-token {kv} prefix with NaN cache rows past the length")
+    cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=512, context=1152,
                              dtype="bf16")
     ref, gpu = build_pair(cfg, root=(44, 0), scale=0.05, kv_dtype=KV_DTYPES[kv])
-    B, P, hd, stale = batch, 1024, cfg.head_dim, 40
+    B, P, hd, stale = batch, prefix, cfg.head_dim, 40
     rc, gc = ref.make_cache(B), gpu.cache()
     dev = ct.device("gpu")
     if KV_DTYPES[kv] == ct.BF16:
