@@ -157,6 +157,7 @@ SIGNATURES = {
     "dl_decoder_lm_generate": (_st, [_p, _p, _p, _i64, _f64, RandomKey, _i32, _pp, _pp]),
     "dl_decoder_lm_benchmark": (_st, [_p, _p, _p, _i64, _i64, _f64, RandomKey, _i32, C.POINTER(_f64), _pp]),
     "dl_decoder_lm_profile": (_st, [_p, _p, _p, _i64, C.POINTER(KernelTiming), C.c_size_t, C.POINTER(C.c_size_t)]),
+    "dl_decoder_lm_set_weight_repack": (_st, [_p, _i32]),
     "dl_sample": (_st, [_p, _f64, RandomKey, _pp]),
     "dl_normal_with_key": (_st, [RandomKey, Shape, _f64, TensorOptions, _pp]),
     "dl_timer_create": (_st, [Device, _pp]),
@@ -482,6 +483,10 @@ class DecoderLM:
         check(lib().dl_decoder_lm_profile(self.handle, t.handle, cache.handle, rounds, out, 32, C.byref(n)))
         return [{"name": out[i].name.decode(), "launches": out[i].launches, "total_ms": out[i].total_ms,
                  "bytes": out[i].bytes} for i in range(n.value)]
+
+    def set_weight_repack(self, enabled: bool) -> None:
+        """Whether batched decode reads a repacked second copy of every bf16 weight (off: the copies are dropped)."""
+        check(lib().dl_decoder_lm_set_weight_repack(self.handle, int(enabled)))
 
 
 class Timer:

@@ -88,6 +88,10 @@ dl_status dl_decoder_lm_profile(dl_decoder_lm* lm, const dl_tensor* ids, dl_deco
     });
 }
 
+dl_status dl_decoder_lm_set_weight_repack(dl_decoder_lm* lm, int32_t enabled) {
+    return invoke([&] { require(lm, "lm").value->set_weight_repack(enabled != 0); });
+}
+
 dl_status dl_sample(const dl_tensor* logits, double temperature, dl_random_key key, dl_tensor** output) {
     return make_handle(output, [&] { return dl::sample(require(logits, "logits").value, temperature, convert(key)); });
 }

@@ -38,6 +38,8 @@ struct DecodeWorkspace {
     /// The packed tiles of `w0` [rows, K] (with `w1`: gate and up, interleaved for the SwiGLU launch), or null
     /// (packing off, not bf16, a shape the pack does not cover, or no current pack while `stream` captures).
     const void* tiles_of(const Tensor& w0, const Tensor* w1, dlh_stream stream);
+    /// Drops every packed copy (their memory returns to the pool once no launch uses it).
+    void release_packs() { packed_.clear(); }
 
 private:
     struct Packed {

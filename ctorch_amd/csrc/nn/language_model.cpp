@@ -31,6 +31,15 @@ DecoderLM::DecoderLM(std::shared_ptr<nn::Embedding> embedding, std::shared_ptr<n
 
 DecoderLM::~DecoderLM() { release_graph(); }
 
+void DecoderLM::set_weight_repack(bool enabled) {
+    ws_.pack_weights = enabled;
+    if (!enabled) {
+        // launches already queued may still read the packed copies: they finish before the memory is returned
+        hip_check(dlh_stream_synchronize(context_->stream), "weight repack off");
+        ws_.release_packs();
+    }
+}
+
 void DecoderLM::release_graph() {
     if (graph_) {
         (void)dlh_stream_synchronize(context_->stream);

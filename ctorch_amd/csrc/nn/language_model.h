@@ -28,6 +28,9 @@ public:
     std::pair<Tensor, Tensor> generate(const Tensor& prompt, std::span<nn::KVCache> cache, Index steps,
                                        double temperature, RandomKey key, bool use_graph);
     std::vector<KernelTiming> profile(const Tensor& ids, std::span<nn::KVCache> cache, Index rounds);
+    /// Whether batched decode (3 to 64 rows) reads a second, repacked copy of every bf16 weight (on by default:
+    /// faster, at the cost of that copy's memory).  Turning it off drops the copies now held.
+    void set_weight_repack(bool enabled);
     /// Prompt, then warmup + timed single-token steps; the last `timed` steps are bracketed by HIP events on
     /// the compute stream (after a synchronize) and their device time is returned in milliseconds.
     double benchmark(const Tensor& prompt, std::span<nn::KVCache> cache, Index warmup, Index timed,

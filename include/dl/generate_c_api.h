@@ -63,6 +63,14 @@ typedef struct dl_kernel_timing {
 DL_API dl_status dl_decoder_lm_profile(dl_decoder_lm* lm, const dl_tensor* ids, dl_decoder_cache* cache,
     int64_t rounds, dl_kernel_timing* timings, size_t capacity, size_t* count);
 
+/* Whether batched decode (3 to 64 rows per step) reads a second copy of every bf16 weight, repacked in the
+ * matrix-core kernel's tile order (1.6 GB for a 1B model, 14 GB for an 8B one; built on the first batched step).
+ * On by default.  enabled = 0 drops the copies held now (after the work already queued that reads them) and has
+ * batched decode read the weights as stored: the same results bit for bit, slower (measured on MI355X at batch
+ * 32, 1B: 1.17 -> 1.40 ms a step, 1.57 GB freed).  Batch-1 decode never builds the copies.  No reference counterpart: for serving processes that need the
+ * memory. */
+DL_API dl_status dl_decoder_lm_set_weight_repack(dl_decoder_lm* lm, int32_t enabled);
+
 /* One index per row of logits [B, V] (f32 or bf16, GPU): temperature <= 0 is the reference argmax rule;
  * otherwise Gumbel-max argmax_i(logit_i / T + g_i), g = -log(-log u), u from Philox(key, b*V + i) on (0, 1),
  * evaluated with basic IEEE double operations so that any restatement gives the same index.  [B] i64. */

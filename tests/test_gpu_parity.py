@@ -301,6 +301,29 @@ def test_batched_decode_on_matrix_cores():
     assert np.array_equal(oracle.sample(l1, 1.0, oracle.fold_in((3, 4), 9)), t1[:, -1])
 
 
+def test_batched_decode_without_the_repacked_weight_copies_gives_the_same_bits_and_frees_them():
+    # dl_decoder_lm_set_weight_repack(0): batched decode reads the weights as stored, and the repacked copies held
+    # so far go back to the pool (at least gate/up and down of every layer: widths the matrix-core path takes)
+    say("case: B=8 bf16 decode with the weight repack on, off and on again")
+    cfg = oracle.ModelConfig(vocab=1024, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=1536, context=64,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(47, 0), scale=0.05)
+    prompt = oracle.random_ids((48, 0), 8 * 16, cfg.vocab).reshape(8, 16)
+    t1, l1 = gpu.generate(prompt, 12)  # repack on (the default): the copies are built on the first batched step
+    held = ct.memory_stats().used_bytes
+    gpu.lm.set_weight_repack(False)
+    freed = held - ct.memory_stats().used_bytes
+    assert freed >= cfg.layers * 3 * cfg.hidden * cfg.dimensions * 2, freed
+    t2, l2 = gpu.generate(prompt, 12)
+    assert np.array_equal(t2, t1) and np.array_equal(l2, l1)
+    gpu.lm.set_weight_repack(True)
+    t3, l3 = gpu.generate(prompt, 12)
+    assert np.array_equal(t3, t1) and np.array_equal(l3, l1)
+    history = np.concatenate([prompt, t1[:, :-1]], 1)
+    want = ref.logits(history, ref.make_cache(8))[:, -1]
+    assert np.max(np.abs(l1 - want)) <= 2e-2
+
+
 def test_batched_decode_reads_weights_loaded_after_its_repacked_copies_were_built():
     say("case: B=4 bf16 decode (repacked projection weights), then new decoder weights loaded, decode again")
     cfg = oracle.ModelConfig(vocab=1000, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=1024, context=32,
