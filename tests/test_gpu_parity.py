@@ -14,7 +14,7 @@ import pytest
 
 import ctorch_amd as ct
 import oracle
-from common import KV_DTYPES, GpuLM, build_pair, rel_err, seed_prefix
+from common import KV_DTYPES, GpuLM, build_pair, greedy_steps, rel_err, seed_prefix
 
 pytestmark = pytest.mark.gpu
 GPU = ct.device("gpu")
@@ -299,6 +299,25 @@ def test_batched_decode_on_matrix_cores():
     t2, l2 = gpu.generate(prompt, 10, 1.0, (3, 4), use_graph=False)
     assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
     assert np.array_equal(oracle.sample(l1, 1.0, oracle.fold_in((3, 4), 9)), t1[:, -1])
+
+
+def test_batched_decode_of_48_sequences_on_four_activation_tiles():
+    # 33-64 rows per launch: four 16-row activation tiles, the last 16 rows past the batch (masked), through the
+    # deep pipeline at K = 512 and 1536 and the LM head at 64-wide chunks
+    say("case: B=48 bf16 decode, d=512 (four activation tiles per projection launch)")
+    cfg = oracle.ModelConfig(vocab=1024, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=1536, context=32,
+                             dtype="bf16")
+    ref, gpu = build_pair(cfg, root=(49, 0), scale=0.05)
+    B = 48
+    prompt = oracle.random_ids((50, 0), B * 6, cfg.vocab).reshape(B, 6)
+    rc, gc = ref.make_cache(B), gpu.cache()
+    want = ref.logits(prompt, rc)[:, -1]
+    got = gpu.logits(prompt, gc)
+    assert np.max(np.abs(got - want)) <= 2e-2
+    greedy_steps(ref, gpu, rc, gc, want.argmax(-1).reshape(B, 1), 3, "B=48")
+    t1, l1 = gpu.generate(prompt, 8, 0.0, (0, 0), use_graph=True)
+    t2, l2 = gpu.generate(prompt, 8, 0.0, (0, 0), use_graph=False)
+    assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
 
 
 def test_batched_decode_without_the_repacked_weight_copies_gives_the_same_bits_and_frees_them():
