@@ -19,6 +19,26 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Every 64-byte line of a kernel's argument block (BYTES of explicit arguments, then the line of the implicit
+// ones the runtime appends: grid and group sizes) requested at once, at entry.  The compiler loads each argument
+// where it is first used, so the lines of a large parameter struct arrive in several dependent scalar round trips
+// (a branch's operand, then the next block's pointers, ...), and between the steps of a decode the weight stream
+// has evicted them from the caches; touched together here they cost one round trip, and the later loads hit.
+template <int EXPLICIT>
+__device__ __forceinline__ void touch_kernargs() {
+    constexpr int LINES = ((EXPLICIT + 7) / 8 * 8 + 64 + 63) / 64;
+    static_assert(LINES <= 10, "one operand per line below");
+    typedef const __attribute__((address_space(4))) uint32_t KernargWord;
+    KernargWord* words = (KernargWord*)__builtin_amdgcn_kernarg_segment_ptr();
+    // one word of each line, all consumed by a single statement: a scalar load's result waits for every scalar
+    // load in flight, so one use point keeps them in one round trip
+    uint32_t v[10];
+#pragma unroll
+    for (int i = 0; i < 10; ++i) v[i] = words[16 * (i < LINES ? i : LINES - 1)];
+    __asm__ volatile("" ::"s"(v[0]), "s"(v[1]), "s"(v[2]), "s"(v[3]), "s"(v[4]), "s"(v[5]), "s"(v[6]), "s"(v[7]),
+                     "s"(v[8]), "s"(v[9]));
+}
+
 // wait until at most n vector-memory operations of this wave are outstanding (lgkm and exp counts untouched)
 template <int N>
 __device__ __forceinline__ void wait_vm() {

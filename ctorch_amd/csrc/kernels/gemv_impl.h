@@ -410,6 +410,9 @@ __device__ __forceinline__ void stream_steps(int count, Buf& a, Buf& b, Load&& l
 // in-wave; on MI355X this beat staging the rows once per work-group in LDS at every decode shape.
 template <typename WT, int MT, int R, int CPI, int EPI, bool NORM>
 __global__ __launch_bounds__(kThreads) void gemv_reg(const dlk_gemv_params p) {
+    // measured on MI355X (A/B against byte-identical builds): the C2 step 547 -> 542 us; the same touch in the
+    // batched projections, the reduce and the decode attention made C2 and C4 slower (C4 9.32 -> 9.56 ms)
+    touch_kernargs<sizeof(dlk_gemv_params)>();
     using Traits = WeightTraits<WT>;
     constexpr int CH = Traits::chunk;
     constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
