@@ -17,13 +17,14 @@
 //
 // Operands reach LDS by the 16-byte global->LDS DMA (lane i of a DMA instruction lands at LDS base + 16 i), in
 // fragment order: for each 16-row tile and 32-wide k step the 16 bytes that MFMA lane l needs sit at 16 l, so the
-// fragment reads are linear and conflict-free and no register staging is needed.  A ring of kStages k steps is
-// in flight.  The global->LDS traffic (48 KB per k step per work-group) is what bounds the kernel, hence the
-// largest tile the LDS ring and the registers hold.
+// fragment reads are linear and conflict-free and no register staging is needed.  Two rings are in flight:
+// weights two k pairs ahead (issued by waves 0-3), activations one k step ahead (waves 4-7).  The global->LDS
+// traffic (48 KB per k step per work-group) and its latency are what bound the kernel, hence the largest tile the
+// LDS rings and the registers hold.
 //
 // Blocks are placed XCD-aware: the hardware hands consecutive work-group ids to the 8 XCDs in turn, so block b
-// takes logical tile (b % 8) * per_xcd + b / 8 and the work-groups of one XCD walk adjacent tiles, which share
-// activation rows and weight rows in that XCD's L2.
+// runs on XCD b % 8, which takes a band of row blocks and walks it in small groups of row blocks column by
+// column, so that the work-groups it runs at once share weight and activation slices in its L2.
 #pragma once
 
 #include "kernels/gemm_rows.h"
@@ -41,16 +42,17 @@ constexpr int kPrepThreads = 256;                  // prepare_rows: one work-gro
 constexpr int kPrepChunk = 512;                    // k per prepare_rows work-group
 constexpr int kBN = 256;                           // weight rows per work-group (16 tiles of 16)
 constexpr int kBM = 256;                           // activation rows per work-group (16 tiles of 16)
-constexpr int kActStages = 3;                      // activation ring: k steps of 32
+constexpr int kActStages = 2;                      // activation ring: k steps of 32
 constexpr int kActBytes = (kBM / 16) * 2048;       // one k step of activation fragments (hi, lo)
-constexpr int kWeightPairBytes = (kBN / 16) * 2048; // weight ring: two buffers of one k pair (64) each
+constexpr int kWeightStages = 3;                   // weight ring: k pairs (64)
+constexpr int kWeightPairBytes = (kBN / 16) * 2048; // one k pair of weight fragments
 constexpr size_t kLdsBytes = 0;                    // the rings are static LDS
-constexpr int kActDma = 2 * (kBM / 16) / kWaves;   // activation DMA instructions per wave per k step
-constexpr int kWeightDma = 2 * (kBN / 16) / kWaves; // weight DMA instructions per wave per k pair
-static_assert(kActStages * kActBytes + 2 * kWeightPairBytes <= 160 * 1024, "LDS");
+constexpr int kActDma = 2 * (kBM / 16) / (kWaves / 2);   // activation DMA instructions per activation wave per k step
+constexpr int kWeightDma = 2 * (kBN / 16) / (kWaves / 2); // weight DMA instructions per weight wave per k pair
+static_assert(kActStages * kActBytes + kWeightStages * kWeightPairBytes <= 160 * 1024, "LDS");
 constexpr int kMinBlocks = 64;                     // one row block of 256 takes the tiled path only this wide
 constexpr int kXcds = 8;
-static_assert(kActDma == 4 && kWeightDma == 4, "per wave: two activation tiles (hi, lo), two weight tiles (two halves)");
+static_assert(kActDma == 8 && kWeightDma == 8, "per wave: four activation tiles (hi, lo), four weight tiles (two halves)");
 
 /// Staging workspace of a launch: the split rows in fragment order, then per-k-chunk sums of squares of each row
 /// (f32 [ceil(K / 512)][M]; the norm factor of row m is 1/sqrt(sum over chunks / K + eps), summed in chunk order).
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(kPrepThreads) void prepare_rows(const dlk_gemv_para
 template <int EPI, bool NORM>
 __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params p) {
     constexpr bool SWIGLU = EPI == DLK_EPI_SWIGLU;
-    __shared__ __attribute__((aligned(1024))) char wring[2][kWeightPairBytes];
+    __shared__ __attribute__((aligned(1024))) char wring[kWeightStages][kWeightPairBytes];
     __shared__ __attribute__((aligned(1024))) char xring[kActStages][kActBytes];
 
     const int t = threadIdx.x, lane = t % kWave;
@@ -204,22 +206,40 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
     const int tiles = gemm::tiles_of(p);
     const int nb = col_blocks(p), total = nb * row_blocks(p);
 
-    // XCD-aware placement: XCD x runs logical tiles [start_x, start_x + count_x) (a sweep of 2 x 32 grouping
-    // shapes for the work-groups one XCD runs at once changed nothing measurable)
+    // XCD-aware placement: XCD x runs logical tiles [start_x, start_x + count_x).  When the row blocks divide
+    // evenly over the XCDs, that range is a band of whole row blocks, and the XCD walks it in groups of GR row
+    // blocks, column by column: its 32 resident work-groups then cover 32 / GR weight blocks and GR row blocks, so
+    // a k step's weight slice is shared by GR of them and its activation slice by 32 / GR (in row order: weights
+    // by none, activations by all 32), and a work-group's share of the L2 misses per k step falls from 17 KB to
+    // 8 KB at GR = 4.  Measured (C5 prefill, A/B against two byte-identical builds): 58.4-58.7 -> 57.6-57.8 ms at
+    // GR 4 or 2, 57.9-58.3 at 8.
     const int per = total / kXcds, rem = total % kXcds;
     const int xcd = blockIdx.x % kXcds, idx = blockIdx.x / kXcds;
     const int logical = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
-    const int n_blk = logical % nb, m_blk = logical / nb;
+    int n_blk = logical % nb, m_blk = logical / nb;
+    const int band_rows = row_blocks(p) % kXcds == 0 ? row_blocks(p) / kXcds : 0;
+    const int GR = band_rows % 4 == 0 ? 4 : band_rows % 2 == 0 ? 2 : 1;
+    if (band_rows > 0 && GR > 1) {
+        const int group = idx / (GR * nb), within = idx % (GR * nb);
+        n_blk = within / GR;
+        m_blk = band_rows * xcd + group * GR + within % GR;
+    }
     const int m_first = m_blk * kBM;
 
     // Weights: a 64-wide k pair of a 16-row tile is 2 KB of LDS, two halves of 8 rows x 128 bytes; each DMA
     // instruction reads 8 whole 128-byte lines (8 lanes per row), which the global->LDS path serves ~3.7x faster
     // than 16 half lines.  Row R of the tile keeps its 16-byte column g at slot g ^ (R >> 1) (XOR swizzle), so
-    // the 16 lanes of an MFMA fragment read (rows 0..15, one column) hit 16 different bank groups.  Wave w fills
-    // tiles 2w, 2w+1 (both halves).
-    const char* wbase[2];
+    // the 16 lanes of an MFMA fragment read (rows 0..15, one column) hit 16 different bank groups.
+    //
+    // Waves 0-3 issue the weight DMAs and waves 4-7 the activation DMAs, so that each wave's in-order count of
+    // loads in flight tracks one stream: a weight wave can wait for pair p while pair p + 1 stays in flight, with
+    // no activation request behind it.  Weight wave r fills tiles 4r .. +4 (both halves), activation wave r
+    // activation tiles 4r .. +4 (hi and lo).
+    const bool weight_wave = wave < kWaves / 2;
+    const int role = weight_wave ? wave : wave - kWaves / 2;
+    const char* wbase[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) wbase[j] = tile_base<SWIGLU>(p, n_blk, 2 * wave + j, tiles);
+    for (int j = 0; j < 4; ++j) wbase[j] = tile_base<SWIGLU>(p, n_blk, 4 * role + j, tiles);
     uint32_t woff[2]; // per half h: lane i -> row 8 h + i / 8, slot i % 8 <- column (i % 8) ^ ((8 h + i / 8) >> 1)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -228,23 +248,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
     }
     // activation tiles in the staging workspace's fragment order: (tile, step) is 2 KB (hi, lo) at
     // ((tile * nsteps) + step) * 2048 (rows past M hold whatever was there: their results are never stored)
-    const char* xbase[2];
+    const char* xbase[4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-        xbase[h] = static_cast<const char*>(p.stage) + static_cast<int64_t>(m_first / 16 + 2 * wave + h) * nsteps * 2048;
+    for (int h = 0; h < 4; ++h)
+        xbase[h] = static_cast<const char*>(p.stage) + static_cast<int64_t>(m_first / 16 + 4 * role + h) * nsteps * 2048;
     const uint32_t xoff = 16 * lane;
-    auto issue_weights = [&](int pair, char* buf) {
+    // half H (0, 1) of a weight wave's share of pair `pair`: tiles 4r + 2H, 4r + 2H + 1
+    auto issue_weights = [&](int pair, auto half_tag, char* buf) {
+        constexpr int H = decltype(half_tag)::value;
         const uint32_t b = lds_offset(buf);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) dma16(wbase[j] + 128 * pair, woff[h], b + (2 * wave + j) * 2048 + h * 1024);
+            for (int h = 0; h < 2; ++h)
+                dma16(wbase[2 * H + j] + 128 * pair, woff[h], b + (4 * role + 2 * H + j) * 2048 + h * 1024);
     };
     auto issue_acts = [&](int step, char* buf) {
         const uint32_t b = lds_offset(buf);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t dst = b + (2 * wave + h) * 2048;
+        for (int h = 0; h < 4; ++h) {
+            const uint32_t dst = b + (4 * role + h) * 2048;
             dma16(xbase[h] + 2048 * step, xoff, dst);
             dma16(xbase[h] + 2048 * step + 1024, xoff, dst + 1024);
         }
@@ -286,48 +309,54 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
         }
     };
 
-    // Two rings.  Activations: three buffers of one k step; weights: two buffers of one k pair.  Step j issues,
-    // after its barrier, the weights of pair j/2 + 1 (even j only: its buffer held pair j/2 - 1, which every wave
-    // finished before this barrier) and the activations of step j + 2 (into the buffer of step j - 1).  Before
-    // step c's barrier a wave waits until only step c-1's DMAs are in flight (8 after an even step, 4 after an
-    // odd one), so its own DMAs of step c's data are done; the barrier makes every wave's visible.  Issues past
-    // the end repeat the last pair or step into a buffer nobody reads again, keeping the counts uniform.  The
-    // prologue issues what steps -2 and -1 would.  nsteps is even.
+    // Two rings.  Weights: three buffers of one k pair.  A weight wave issues pair p + 2 in two halves, after its
+    // products of steps 2p and 2p + 1, into the buffer of pair p - 1 (which every wave finished before the
+    // barrier of step 2p), and at the end of step 2p + 1 waits until only those DMAs are in flight, so pair p + 1
+    // has landed before the barrier of step 2p + 2: about four k steps of lead for the operand that comes from
+    // the last-level cache or HBM.  Activations: two buffers of one k step; an activation wave issues
+    // step c + 1 right after the barrier of step c (into the buffer of step c - 1) and waits for it before the
+    // next barrier: one step of lead for rows that a group of work-groups shares in its L2.  Issues past the end
+    // repeat the last pair or step into a buffer nobody reads again, keeping the counts uniform.  A SIMD holds
+    // waves w and w + 4, one of each kind, so one issues its DMAs before its products and the other after them.
+    // nsteps is even.
     const int npairs = nsteps / 2;
-    issue_weights(0, wring[0]);
-    issue_acts(0, xring[0]);
-    issue_acts(min(1, nsteps - 1), xring[1]);
-    // Waves 0-3 issue a step's DMAs before its products and waves 4-7 after them (wave w and w + 4 share a SIMD
-    // on MI355X), so the two waves of a SIMD do not both sit in the DMA issue while its matrix core idles
-    // (measured: C5 prefill 55.1 -> 54.7 ms, A/B on one box).  Each wave's DMAs keep their order and counts, so
-    // the waits below are unchanged, and every DMA still follows the barrier after which nobody reads the buffer
-    // it fills.
-    const bool early = wave < kWaves / 2;
-    int xb = 0;
+    using H0 = std::integral_constant<int, 0>;
+    using H1 = std::integral_constant<int, 1>;
+    if (weight_wave) {
+        issue_weights(0, H0{}, wring[0]);
+        issue_weights(0, H1{}, wring[0]);
+        issue_weights(min(1, npairs - 1), H0{}, wring[1]);
+        issue_weights(min(1, npairs - 1), H1{}, wring[1]);
+        wait_vm<kWeightDma>();
+    } else {
+        issue_acts(0, xring[0]);
+        wait_vm<0>();
+    }
+    ring_barrier();
+    int wb = 0; // buffer of the current pair
     for (int c = 0; c < nsteps; c += 2) {
         const int pair = c / 2;
-        // even step c: weights pair `pair` (first half of its k), activations of step c
-        wait_vm<kActDma>();
+        const int wnext = wb == 0 ? kWeightStages - 1 : wb - 1; // pair + 2 takes the buffer of pair - 1
+        // even step c
+        if (!weight_wave) issue_acts(min(c + 1, nsteps - 1), xring[1]);
+        compute(wring[wb], 0, xring[0]);
+        if (weight_wave) {
+            issue_weights(min(pair + 2, npairs - 1), H0{}, wring[wnext]);
+        } else {
+            wait_vm<0>();
+        }
         ring_barrier();
-        const int xe = xb == 0 ? kActStages - 1 : xb - 1;
-        if (early) {
-            issue_weights(min(pair + 1, npairs - 1), wring[(pair + 1) & 1]);
-            issue_acts(min(c + 2, nsteps - 1), xring[xe]);
-        }
-        compute(wring[pair & 1], 0, xring[xb]);
-        if (!early) {
-            issue_weights(min(pair + 1, npairs - 1), wring[(pair + 1) & 1]);
-            issue_acts(min(c + 2, nsteps - 1), xring[xe]);
-        }
-        xb = xb + 1 == kActStages ? 0 : xb + 1;
         // odd step c + 1
-        wait_vm<kActDma + kWeightDma>();
+        if (!weight_wave) issue_acts(min(c + 2, nsteps - 1), xring[0]);
+        compute(wring[wb], 1, xring[1]);
+        if (weight_wave) {
+            issue_weights(min(pair + 2, npairs - 1), H1{}, wring[wnext]);
+            wait_vm<kWeightDma>();
+        } else {
+            wait_vm<0>();
+        }
         ring_barrier();
-        const int xo = xb == 0 ? kActStages - 1 : xb - 1;
-        if (early) issue_acts(min(c + 3, nsteps - 1), xring[xo]);
-        compute(wring[pair & 1], 1, xring[xb]);
-        if (!early) issue_acts(min(c + 3, nsteps - 1), xring[xo]);
-        xb = xb + 1 == kActStages ? 0 : xb + 1;
+        wb = wb + 1 == kWeightStages ? 0 : wb + 1;
     }
     wait_vm<0>();
 
