@@ -33,6 +33,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRows = 128;  // query rows per work-group
 constexpr int kKeys = 64;   // keys per tile
+constexpr int kXcds = 8;    // XCDs of the MI355X: linear work-group id i runs on XCD i % 8
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -187,8 +188,19 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
     const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
     const int G = p.H / p.KV, per_head = kRows / G;
     const int blocks = (p.L + per_head - 1) / per_head;
-    const int qb = blocks - 1 - static_cast<int>(blockIdx.x); // the longest key ranges start first
-    const int b = static_cast<int>(blockIdx.y) / p.KV, kvh = static_cast<int>(blockIdx.y) % p.KV;
+    // XCD-aware order: the hardware hands linear work-group id i to XCD i % 8, so with the (sequence, KV head)
+    // pairs a multiple of 8, pair j's query blocks all run on XCD j % 8, the next pair of that XCD following once
+    // they are done: the XCD's L2 then holds the K/V tiles of one or two pairs, which its work-groups share, not
+    // those of every pair
+    int qx = static_cast<int>(blockIdx.x), pair = static_cast<int>(blockIdx.y);
+    if (gridDim.y % kXcds == 0) {
+        const int linear = qx + static_cast<int>(gridDim.x) * pair;
+        const int xcd = linear % kXcds, idx = linear / kXcds;
+        pair = xcd + kXcds * (idx / static_cast<int>(gridDim.x));
+        qx = idx % static_cast<int>(gridDim.x);
+    }
+    const int qb = blocks - 1 - qx; // the longest key ranges start first
+    const int b = pair / p.KV, kvh = pair % p.KV;
     const int first = static_cast<int>(p.position ? *p.position : p.first_host);
     const int S = first + p.L;
     const int l0 = qb * per_head;
@@ -301,7 +313,7 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
             using T = SplitTile<HD>;
             static_assert(T::KSTRIDE == KSTRIDE && T::VSTRIDE == VSTRIDE, "one layout");
             const char* src = static_cast<const char*>(p.kv_split) +
-                              (static_cast<int64_t>(blockIdx.y) * p.kv_split_tiles + tile) * T::BYTES +
+                              (static_cast<int64_t>(pair) * p.kv_split_tiles + tile) * T::BYTES +
                               (wave < 2 ? wave * T::KPLANE : 2 * T::KPLANE + (wave - 2) * T::VPLANE);
             const uint32_t lds = lds_offset(wave < 2 ? &ks[wave][buf][0] : &vt[wave - 2][buf][0]);
             const int blocks = (wave < 2 ? T::KPLANE : T::VPLANE) / 1024;
