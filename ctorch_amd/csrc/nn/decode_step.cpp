@@ -266,7 +266,8 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         // fit one per CU: the attention finishes the projection from its partials (sums them, normalises,
         // rotates, appends K/V), which drops the reduce launch.  Every work-group pays the partials' round trip
         // before its first tile, so a grid of several work-groups per CU (MI355X, 8B at b=8 over 32768 keys:
-        // 10.2 -> 10.8 ms a step) keeps the reduce launch; at one per CU (1B at b=32: 1.49 -> 1.45 ms) it pays.
+        // 10.2 -> 10.8 ms a step; measured again with the first tile requested before the length, 9.31 -> 9.84 ms)
+        // keeps the reduce launch; at one per CU (1B at b=32: 1.49 -> 1.45 ms) it pays.
         const bool one_per_cu = static_cast<int64_t>(a.splits) * batch * KV <= 256;
         const int qkv_splits = length == 1 && !adapters[0] && !adapters[1] && !a.stage_out && one_per_cu
                                    ? dlk_gemv_split_count(&qkv)
