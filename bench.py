@@ -31,7 +31,7 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per launch of the gate/up kernel: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE per dispatch, each scaled
 # by what the counter reads for this script's 1 GiB copy probe (x2.0 and x1.0); the commands and the table are in
 # the traffic summary under profiles/.  A measurement of the kernel as built, not derived from the bytes below.
-GATE_UP_TRAFFIC_BYTES = 46_364_877 + 45_056
+GATE_UP_TRAFFIC_BYTES = 46_372_045 + 45_056
 C2 = dict(vocab=32000, layers=16, dimensions=2048, heads=32, kv_heads=8, hidden=5632)
 C4 = dict(vocab=32000, layers=32, dimensions=4096, heads=32, kv_heads=8, hidden=14336, rope_base=500000.0)
 C5 = dict(C2, lora_rank=16, lora_alpha=32.0)
