@@ -544,6 +544,34 @@ def test_prefill_on_tiled_matrix_cores_with_lora_and_causal_attention(kv):
     assert rel_err(again, full) <= 1e-4
 
 
+def test_prefill_of_four_sequences_takes_the_tiled_projection_in_groups_of_four_row_blocks():
+    # 4 x 2048 rows are 32 row blocks of 256: each XCD takes a band of 4 and walks it in one group of 4 row blocks
+    # (the C5 order); two chunks of 1024 per sequence (16 row blocks, groups of 2) must give the same logits, and
+    # the 8 (sequence, KV head) pairs take the prefill attention's one-XCD-per-pair order
+    say("case: bf16 prefill B=4 x 2048, d=512, LoRA q/v, f32 K/V: tiled projections in groups of 4 row blocks")
+    cfg = oracle.ModelConfig(vocab=512, layers=1, dimensions=512, heads=8, kv_heads=2, hidden=1536, context=2056,
+                             dtype="bf16", lora_rank=16, lora_alpha=32.0)
+    ref, gpu = build_pair(cfg, root=(64, 0), scale=0.03)
+    B, P = 4, 2048
+    prompt = oracle.random_ids((65, 0), B * P, cfg.vocab).reshape(B, P)
+    rc, gc = ref.make_cache(B), gpu.cache()
+    want = ref.logits(prompt, rc)[:, -1]
+    got = gpu.logits(prompt, gc)
+    say(f"  prefill logits: max|d| {np.max(np.abs(got - want)):.3g}, rel {rel_err(got, want):.3g}")
+    assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4
+    ids = want.argmax(-1).reshape(B, 1)
+    for step in range(2):  # decode over the keys the tiled QKV epilogue wrote
+        want = ref.logits(ids, rc)[:, -1]
+        got = gpu.logits(ids, gc)
+        assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4, step
+        ids = want.argmax(-1).reshape(B, 1)
+    full = gpu.logits(prompt, gpu.cache())
+    chunked_cache = gpu.cache()
+    gpu.logits(prompt[:, :1024], chunked_cache)
+    chunked = gpu.logits(prompt[:, 1024:], chunked_cache)
+    assert rel_err(chunked, full) <= 1e-4
+
+
 def test_graph_decode_at_a_capacity_far_above_the_length_ignores_stale_workspace_memory():
     # graph replay sizes the key splits for the cache capacity, so most splits hold no keys and never write their
     # partial output rows; the merge must not read them.  The pool is first filled with NaN blocks and released, so
