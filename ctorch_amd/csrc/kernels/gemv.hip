@@ -192,7 +192,8 @@ int resident_waves(const Kernel& kernel) {
 // second group's weights are in flight while the first is reduced.  Measured on MI355X under graph replay at
 // the 1B decode shapes (groups 1536 / 2816 / 2048 for QKV, gate/up, down): 6.04 -> 5.62, 10.83 -> 10.14 and
 // 7.31 -> 6.26 us; with 1024 groups (O projection) one per wave stays faster (3.76 vs 4.45 us).  Three or four
-// groups per wave were slower: a C2 step 541 -> 553 / 591 us.
+// groups per wave were slower (a C2 step 541 -> 553 / 591 us), and so were work-groups of two waves instead of four
+// (543 -> 558 us).
 int launch_waves(const dlk_gemv_params& p) {
     using namespace dlk::gemv;
     constexpr int kPairedGroups = 1536;
