@@ -520,6 +520,98 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
     }
 }
 
+// Narrow projections over staged rows (STORE, at most two 16-row weight tiles: the LoRA down projections of q and v,
+// 2 x 16 rows): gemm_tiles would give each 256-row block one work-group of mostly idle waves (64 work-groups for
+// 16384 rows, streaming the rows at ~2 TB/s).  Here each wave takes one 16-row tile of the staged rows and reads
+// its hi and lo fragments straight from the staging workspace (1 KB contiguous per fragment, no LDS), with the
+// weight fragments (a few KB per k step, hot in the L2) from the weights as stored; the norm factor scales the
+// finished dots as in gemm_tiles.
+constexpr int kNarrowWaves = 4; // waves (16-row tiles) per work-group
+constexpr int kNarrowBatch = 4; // k steps per batch of loads (two batches in flight)
+
+/// Whether a tiled-eligible launch takes gemm_narrow (host side).
+inline bool narrow_eligible(const dlk_gemv_params& p) {
+    return p.epilogue == DLK_EPI_STORE && !p.bias && gemm::tiles_of(p) <= 2;
+}
+
+template <bool NORM>
+__global__ __launch_bounds__(kNarrowWaves * kWave) void gemm_narrow(const dlk_gemv_params p) {
+    const int lane = threadIdx.x % kWave, q = lane / 16, r = lane % 16;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int mt = blockIdx.x * kNarrowWaves + wave; // this wave's 16-row tile
+    if (mt * 16 >= p.M) return;                       // wave-uniform; no barrier follows
+    const int K = p.K, nsteps = K / 32, tiles = gemm::tiles_of(p);
+    // weight fragment of tile t, k step s: row r of the tile, columns 32 s + 8 q .. +8 (the second tile repeats
+    // the first when there is one tile; its products are then not stored)
+    const gemm::TileMap t0 = gemm::locate<false>(p, 0), t1 = gemm::locate<false>(p, min(1, tiles - 1));
+    const uint16_t* w0 = gemm::tile_row<false>(t0, r, K) + 8 * q;
+    const uint16_t* w1 = gemm::tile_row<false>(t1, r, K) + 8 * q;
+    const char* xs = static_cast<const char*>(p.stage) + static_cast<int64_t>(mt) * nsteps * 2048 + 16 * lane;
+    struct Frag {
+        bf16x8 bh, bl, a0, a1;
+    };
+    auto load = [&](int step, Frag& f) {
+        f.bh = *reinterpret_cast<const bf16x8*>(xs + static_cast<int64_t>(step) * 2048);
+        f.bl = *reinterpret_cast<const bf16x8*>(xs + static_cast<int64_t>(step) * 2048 + 1024);
+        f.a0 = *reinterpret_cast<const bf16x8*>(w0 + 32 * step);
+        f.a1 = *reinterpret_cast<const bf16x8*>(w1 + 32 * step);
+    };
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    auto products = [&](const Frag& f) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a0, f.bh, acc0, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a0, f.bl, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a1, f.bh, acc1, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.a1, f.bl, acc1, 0, 0, 0);
+    };
+    // batches of kNarrowBatch k steps, two in flight: batch b + 1's loads go out before batch b's products (loads
+    // past the end repeat the last step and are not used)
+    constexpr int NB = kNarrowBatch;
+    const int batches = nsteps / NB;
+    Frag fa[NB], fb[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) load(min(u, nsteps - 1), fa[u]);
+    int b = 0;
+    for (; b + 2 <= batches; b += 2) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) load(min((b + 1) * NB + u, nsteps - 1), fb[u]);
+#pragma unroll
+        for (int u = 0; u < NB; ++u) products(fa[u]);
+#pragma unroll
+        for (int u = 0; u < NB; ++u) load(min((b + 2) * NB + u, nsteps - 1), fa[u]);
+#pragma unroll
+        for (int u = 0; u < NB; ++u) products(fb[u]);
+    }
+    if (b < batches) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) products(fa[u]);
+    }
+    for (int step = batches * NB; step < nsteps; ++step) {
+        Frag f;
+        load(step, f);
+        products(f);
+    }
+    // lane holds D[weight rows 4 q .. +4][activation row r] of each tile
+    const int m = 16 * mt + r;
+    if (m >= p.M) return;
+    const float scale = (NORM && p.apply_norm ? stage_inv(p, m) : 1.0f) * p.acc_scale;
+    const int n0 = gemv::seg_column(p, t0.seg) + t0.n0 + 4 * q;
+    *reinterpret_cast<float4*>(p.y + static_cast<int64_t>(m) * p.ldy + n0) =
+        make_float4(acc0[0] * scale, acc0[1] * scale, acc0[2] * scale, acc0[3] * scale);
+    if (tiles > 1) {
+        const int n1 = gemv::seg_column(p, t1.seg) + t1.n0 + 4 * q;
+        *reinterpret_cast<float4*>(p.y + static_cast<int64_t>(m) * p.ldy + n1) =
+            make_float4(acc1[0] * scale, acc1[1] * scale, acc1[2] * scale, acc1[3] * scale);
+    }
+}
+
+/// The narrow kernel for a STORE launch that takes it; {} otherwise.
+inline gemv::Kernel resolve_narrow(const dlk_gemv_params& p) {
+    if (!narrow_eligible(p)) return {};
+    if (gemv::norm_variant(DLK_EPI_STORE, p.apply_norm != 0))
+        return {reinterpret_cast<const void*>(&gemm_narrow<true>), 0};
+    return {reinterpret_cast<const void*>(&gemm_narrow<false>), 0};
+}
+
 /// The tiled kernel for these parameters; {} if none.
 template <int EPI>
 gemv::Kernel resolve(const dlk_gemv_params& p) {
@@ -540,6 +632,7 @@ gemv::Kernel resolve(const dlk_gemv_params& p) {
 } // namespace dlk::tiles
 
 dlk::gemv::Kernel dlk_tiles_kernel_store(const dlk_gemv_params& p);
+dlk::gemv::Kernel dlk_tiles_kernel_narrow(const dlk_gemv_params& p);
 dlk::gemv::Kernel dlk_tiles_kernel_residual(const dlk_gemv_params& p);
 dlk::gemv::Kernel dlk_tiles_kernel_qkv(const dlk_gemv_params& p);
 dlk::gemv::Kernel dlk_tiles_kernel_swiglu(const dlk_gemv_params& p);

@@ -66,11 +66,17 @@ int launch_prepare(const dlk_gemv_params& p, hipStream_t stream);
 // already holds them), then the tiled projection.
 int launch_tiles(const dlk_gemv_params& p, hipStream_t stream) {
     using namespace dlk::tiles;
-    const Kernel kernel = resolve_tiles(p);
+    const Kernel narrow = dlk_tiles_kernel_narrow(p);
+    const Kernel kernel = narrow.fn ? narrow : resolve_tiles(p);
     if (!kernel.fn) return static_cast<int>(hipErrorInvalidValue);
     const int status = launch_prepare(p, stream);
     if (status != 0) return status;
     void* args[] = {const_cast<dlk_gemv_params*>(&p)};
+    if (narrow.fn) {
+        const int waves = (p.M + 15) / 16;
+        return static_cast<int>(hipLaunchKernel(kernel.fn, dim3((waves + kNarrowWaves - 1) / kNarrowWaves),
+                                                dim3(kNarrowWaves * dlk::kWave), args, 0, stream));
+    }
     const int blocks = col_blocks(p) * row_blocks(p);
     return static_cast<int>(hipLaunchKernel(kernel.fn, dim3(blocks), dim3(kThreads), args, kernel.lds, stream));
 }

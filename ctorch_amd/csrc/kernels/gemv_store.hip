@@ -16,3 +16,7 @@ dlk::gemv::Kernel dlk_gemm_reduce_store(const dlk_gemv_params& p) {
 dlk::gemv::Kernel dlk_tiles_kernel_store(const dlk_gemv_params& p) {
     return dlk::tiles::resolve<DLK_EPI_STORE>(p);
 }
+
+dlk::gemv::Kernel dlk_tiles_kernel_narrow(const dlk_gemv_params& p) {
+    return dlk::tiles::resolve_narrow(p);
+}
