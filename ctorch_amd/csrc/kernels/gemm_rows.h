@@ -140,6 +140,7 @@ __device__ __forceinline__ const uint16_t* tile_row(const TileMap& t, int i, int
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4))); // the bf16 operands of v_mfma_f32_16x16x16_bf16
 
 // bf16 hi and lo parts of four values (x = hi + lo to ~2^-16): the hardware's round-to-nearest-even conversion
 // packs two values per instruction, and the hi values are widened back from the packed words by shift and mask
@@ -727,6 +728,21 @@ inline bool wide_eligible(const dlk_gemv_params& p) {
            p.ldx % 4 == 0;
 }
 
+/// A QKV launch on the wide kernel over one activation tile with LoRA down rows (bf16, rank 4..16 in steps of 4,
+/// 16-byte aligned rows) folds the down projections into its key loop.
+inline bool lora_fold_eligible(const dlk_gemv_params& p) {
+    const bool any = p.lora_down[0] || p.lora_down[2];
+    const int r = p.lora_rank;
+    if (p.epilogue != DLK_EPI_QKV || !any || p.lora_down[1] || p.M > 16 || !p.w_bf16 || p.acc_scale != 1.0f ||
+        r < 4 || r > 16 || r % 4 != 0 || !wide_eligible(p))
+        return false;
+    for (int s = 0; s < 3; s += 2)
+        if (p.lora_down[s] && (!p.lora_up[s] || p.lora_hidden[s] || reinterpret_cast<uintptr_t>(p.lora_down[s]) % 16 != 0 ||
+                               reinterpret_cast<uintptr_t>(p.lora_up[s]) % 8 != 0))
+            return false;
+    return true;
+}
+
 template <int EPI, bool NORM, int MT>
 __global__ __launch_bounds__(kWideWaves * kWave) void gemm_wide(const dlk_gemv_params launch) {
     // row_parts: work-group row y takes rows 16 MT y .. +16 MT of the launch (the length advances once)
@@ -779,14 +795,38 @@ __global__ __launch_bounds__(kWideWaves * kWave) void gemm_wide(const dlk_gemv_p
         acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
         squares[mt] = 0.f;
     }
+    // Folded LoRA (QKV over one activation tile, lora_down set for this tile's segment): the down rows (rank <= 16:
+    // one 16-row operand, rows past the rank repeat the last one) take the same activation fragments as the
+    // weights, into a partial hidden tile H_w[r][m] over this wave's keys.  That accumulator's lane layout (rows
+    // 4 (lane / 16) .. +3 of column lane % 16) is the B operand of the 16x16x16 MFMA, so the wave applies the up
+    // rows to its own partial (up . H = sum over waves of up . H_w) and adds scale * up . H_w to acc before the
+    // merge: no hidden rows in memory and no launch for them.  The norm factor and acc_scale then apply to both.
+    constexpr bool FOLD = EPI == DLK_EPI_QKV && MT == 1;
+    const uint16_t* drow = nullptr;
+    u32x2 up_frag = {0u, 0u};
+    f32x4 hacc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (FOLD) {
+        const void* down = tm.seg == 0 ? p.lora_down[0] : tm.seg == 2 ? p.lora_down[2] : nullptr;
+        if (down) {
+            const int rank = p.lora_rank;
+            drow = static_cast<const uint16_t*>(down) + static_cast<int64_t>(min(i16, rank - 1)) * K + kb + 8 * g4;
+            // up rows n0 + lane % 16, ranks 4 (lane / 16) .. +3 (zero past the rank: the A operand)
+            if (4 * g4 < rank)
+                up_frag = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(tm.seg == 0 ? p.lora_up[0]
+                                                                                                   : p.lora_up[2]) +
+                                                          static_cast<int64_t>(tm.n0 + i16) * rank + 4 * g4);
+        }
+    }
     for (int s0 = 0; s0 < steps; s0 += D) {
         // the batch's loads first (steps past the wave's run repeat its last step and are not used)
-        u32x4 wv[D], gv[D][2];
+        u32x4 wv[D], gv[D][2], dv[D];
         float4 xv[D][MT][2];
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int s = min(s0 + d, steps - 1);
             wv[d] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + wstep * s));
+            dv[d] = u32x4{0u, 0u, 0u, 0u};
+            if (FOLD && drow) dv[d] = *reinterpret_cast<const u32x4*>(drow + 32 * s);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 xv[d][mt][0] = *reinterpret_cast<const float4*>(xrow[mt] + 32 * s);
@@ -830,8 +870,25 @@ __global__ __launch_bounds__(kWideWaves * kWave) void gemm_wide(const dlk_gemv_p
                 const u32x4 hh = {h0.x, h0.y, h1.x, h1.y}, ll = {l0.x, l0.y, l1.x, l1.y};
                 acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, hh), acc[mt], 0, 0, 0);
                 acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8, ll), acc[mt], 0, 0, 0);
+                if (FOLD && drow) {
+                    const bf16x8 down = __builtin_bit_cast(bf16x8, dv[d]);
+                    hacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(down, __builtin_bit_cast(bf16x8, hh), hacc, 0, 0, 0);
+                    hacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(down, __builtin_bit_cast(bf16x8, ll), hacc, 0, 0, 0);
+                }
             }
         }
+    }
+    if (FOLD && drow) {
+        // the partial hidden tile as bf16 hi + lo (to 2^-16 of itself), times the up rows
+        const float h[4] = {hacc[0], hacc[1], hacc[2], hacc[3]};
+        u32x2 hi, lo;
+        split4_bf16(h, hi, lo);
+        const s16x4 up = __builtin_bit_cast(s16x4, up_frag);
+        f32x4 l = {0.f, 0.f, 0.f, 0.f};
+        l = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(up, __builtin_bit_cast(s16x4, hi), l, 0, 0, 0);
+        l = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(up, __builtin_bit_cast(s16x4, lo), l, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[0][j] += p.lora_scale * l[j];
     }
     // merge the waves in wave order
 #pragma unroll

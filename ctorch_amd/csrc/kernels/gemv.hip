@@ -252,6 +252,10 @@ extern "C" int dlk_gemv_uses_rows(const dlk_gemv_params* p) {
     return !dlk::tiles::eligible(*p) && dlk::gemm::eligible(*p) ? 1 : 0;
 }
 
+extern "C" int dlk_gemv_folds_lora(const dlk_gemv_params* p) {
+    return !dlk::tiles::eligible(*p) && dlk::gemm::eligible(*p) && dlk::gemm::lora_fold_eligible(*p) ? 1 : 0;
+}
+
 extern "C" int64_t dlk_gemv_split_floats(const dlk_gemv_params* p) {
     if (dlk::tiles::eligible(*p)) return 0;
     if (!dlk::gemm::eligible(*p)) return 0;
@@ -300,6 +304,9 @@ extern "C" int dlk_gemv(const dlk_gemv_params* params, dlh_stream stream_handle)
         return static_cast<int>(hipErrorInvalidValue);
     if (params->defer_reduce && (dlk::tiles::eligible(*params) || !dlk::gemm::eligible(*params) ||
                                  dlk::gemm::wide_eligible(*params)))
+        return static_cast<int>(hipErrorInvalidValue);
+    // only the wide kernel applies LoRA down rows
+    if ((params->lora_down[0] || params->lora_down[1] || params->lora_down[2]) && !dlk_gemv_folds_lora(params))
         return static_cast<int>(hipErrorInvalidValue);
     if (dlk::tiles::eligible(*params)) return launch_tiles(*params, stream);
     if (dlk::gemm::eligible(*params)) return launch_gemm(*params, stream);

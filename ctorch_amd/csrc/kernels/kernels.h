@@ -71,6 +71,8 @@ typedef struct dlk_gemv_params {
     const float* lora_hidden[3]; /* per segment: [M_total, rank] f32 hidden = down(norm(x)) or NULL */
     int64_t lora_ld;             /* row stride of the lora_hidden rows (0: lora_rank) */
     const void* lora_up[3];      /* per segment: [seg_rows, rank] */
+    const void* lora_down[3];    /* per segment: [rank, K] bf16 down rows that the launch applies itself (its
+                                    lora_hidden NULL), when dlk_gemv_folds_lora says it can; else NULL */
     int lora_rank;
     float lora_scale;
     /* STORE / RESIDUAL: device cache length advanced by one thread after the launch's reads of it */
@@ -110,6 +112,10 @@ int dlk_pack_tiles(const void* w0, const void* w1, int swiglu, int64_t rows, int
 /* 1 when dlk_gemv takes a batched matrix-core kernel (gemm_rows or gemm_wide, which read w_tiles) for this
    launch. */
 int dlk_gemv_uses_rows(const dlk_gemv_params* p);
+/* 1 when this QKV launch, with lora_down set for its adapted segments (and their lora_hidden NULL), computes the
+   LoRA down projections itself: a launch over at most 16 rows on the few-row matrix-core kernel, bf16 weights,
+   rank 4..16 in steps of 4, acc_scale 1.  dlk_gemv refuses lora_down otherwise. */
+int dlk_gemv_folds_lora(const dlk_gemv_params* p);
 /* Floats of workspace that lets dlk_gemv split the keys of this launch (0 when it would not split). */
 int64_t dlk_gemv_split_floats(const dlk_gemv_params* p);
 /* Key slices dlk_gemv will use for this launch as attached (1: no split). */

@@ -114,38 +114,12 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         staged = tiled ? p.stage : nullptr;
     };
 
-    // 1. LoRA hidden states (down projections of the normalised input), when adapters are attached: one launch
-    //    for both adapters, their down matrices as two weight segments whose outputs sit side by side in a row
-    //    of ws.lora (query adapter first)
+    // 2. QKV projection: fused RMSNorm prologue, (LoRA,) RoPE and KV append epilogue; issued with the attention.
+    //    Its parameters come first: over few rows the launch may apply the LoRA down rows itself, and then 1 is
+    //    not issued.
     const nn::LoRAAdapter* adapters[2] = {attention.query_adapter(), attention.value_adapter()};
     const Index lora_width = ws.lora.defined() ? ws.lora.size(1) : 0;
-    if (adapters[0] || adapters[1]) {
-        int nb = 0, wb = -1;
-        dlk_gemv_params p = gemv_params(x_in, rows, d, DLK_EPI_STORE);
-        p.apply_norm = 1;
-        p.norm_weight = norm_data(layer.attention_norm(), nb);
-        p.norm_bf16 = nb;
-        p.epsilon = static_cast<float>(layer.attention_norm().epsilon());
-        double bytes = 0.0;
-        for (const auto* adapter : adapters) {
-            if (!adapter) continue;
-            int ab = 0;
-            p.w[p.nseg] = weight_data(adapter->down().weight(), ab, "LoRA down");
-            if (wb >= 0 && ab != wb) throw std::invalid_argument("LoRA adapters must share one dtype");
-            wb = ab;
-            p.seg_rows[p.nseg++] = static_cast<int>(adapter->rank());
-            bytes += static_cast<double>(adapter->down().weight().numel()) * (ab ? 2 : 4);
-        }
-        p.w_bf16 = wb;
-        p.y = static_cast<float*>(mutable_data(ws.lora));
-        p.ldy = lora_width;
-        ws.attach_workspace(p, device);
-        share_stage(p);
-        issue(observer, "lora_down", bytes,
-              [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "LoRA down projection"); });
-    }
-
-    // 2. QKV projection: fused RMSNorm prologue, (LoRA,) RoPE and KV append epilogue; issued with the attention
+    bool lora_folded = false;
     dlk_gemv_params qkv{};
     double qkv_bytes = 0.0;
     {
@@ -175,28 +149,67 @@ void decode_layer(const TransformerDecoderLayer& layer, const float* x_in, float
         p.v_cache = cache.value_data();
         p.cache_bf16 = kv_bf16;
         p.cache_capacity = cache.capacity();
-        if (const auto* a = attention.query_adapter()) {
-            int ub = 0;
-            p.lora_hidden[0] = ws.lora.data<float>();
-            p.lora_up[0] = weight_data(a->up().weight(), ub, "LoRA up");
-            p.lora_rank = static_cast<int>(a->rank());
-            p.lora_scale = static_cast<float>(a->scale());
-        }
-        if (const auto* a = attention.value_adapter()) {
-            int ub = 0;
-            p.lora_hidden[2] = ws.lora.data<float>() + (attention.query_adapter() ? attention.query_adapter()->rank() : 0);
-            p.lora_up[2] = weight_data(a->up().weight(), ub, "LoRA up");
+        bool down_bf16 = true;
+        for (int i = 0; i < 2; ++i) {
+            const nn::LoRAAdapter* a = adapters[i];
+            if (!a) continue;
+            const int seg = 2 * i; // q or v
+            int ub = 0, db = 0;
+            p.lora_hidden[seg] = ws.lora.data<float>() + (i == 1 && adapters[0] ? adapters[0]->rank() : 0);
+            p.lora_up[seg] = weight_data(a->up().weight(), ub, "LoRA up");
+            if (ub != qb) throw std::invalid_argument("LoRA up weights must share the projection dtype");
+            p.lora_down[seg] = weight_data(a->down().weight(), db, "LoRA down");
+            down_bf16 = down_bf16 && db;
             p.lora_rank = static_cast<int>(a->rank());
             p.lora_scale = static_cast<float>(a->scale());
         }
         p.lora_ld = lora_width;
-        if (attention.query_adapter() && attention.value_adapter() &&
-            (attention.query_adapter()->rank() != attention.value_adapter()->rank() ||
-             attention.query_adapter()->scale() != attention.value_adapter()->scale()))
+        if (adapters[0] && adapters[1] &&
+            (adapters[0]->rank() != adapters[1]->rank() || adapters[0]->scale() != adapters[1]->scale()))
             throw std::invalid_argument("query and value adapters must share rank and alpha");
         qkv_bytes = static_cast<double>((H + 2 * KV) * hd * d) * (qb ? 2 : 4) + 2.0 * kv_bytes_per * length;
         ws.attach_workspace(p, device);
+        // the fold reads the down rows in place of the hidden rows of 1
+        if (adapters[0] || adapters[1]) {
+            const float* hidden[2] = {p.lora_hidden[0], p.lora_hidden[2]};
+            p.lora_hidden[0] = p.lora_hidden[2] = nullptr;
+            lora_folded = down_bf16 && dlk_gemv_folds_lora(&p) != 0;
+            if (!lora_folded) {
+                p.lora_hidden[0] = hidden[0];
+                p.lora_hidden[2] = hidden[1];
+                p.lora_down[0] = p.lora_down[2] = nullptr;
+            }
+        }
         qkv = p;
+    }
+
+    // 1. LoRA hidden states (down projections of the normalised input), when adapters are attached and the QKV
+    //    launch does not fold them into its key loop: one launch for both adapters, their down matrices as two
+    //    weight segments whose outputs sit side by side in a row of ws.lora (query adapter first)
+    if ((adapters[0] || adapters[1]) && !lora_folded) {
+        int nb = 0, wb = -1;
+        dlk_gemv_params p = gemv_params(x_in, rows, d, DLK_EPI_STORE);
+        p.apply_norm = 1;
+        p.norm_weight = norm_data(layer.attention_norm(), nb);
+        p.norm_bf16 = nb;
+        p.epsilon = static_cast<float>(layer.attention_norm().epsilon());
+        double bytes = 0.0;
+        for (const auto* adapter : adapters) {
+            if (!adapter) continue;
+            int ab = 0;
+            p.w[p.nseg] = weight_data(adapter->down().weight(), ab, "LoRA down");
+            if (wb >= 0 && ab != wb) throw std::invalid_argument("LoRA adapters must share one dtype");
+            wb = ab;
+            p.seg_rows[p.nseg++] = static_cast<int>(adapter->rank());
+            bytes += static_cast<double>(adapter->down().weight().numel()) * (ab ? 2 : 4);
+        }
+        p.w_bf16 = wb;
+        p.y = static_cast<float*>(mutable_data(ws.lora));
+        p.ldy = lora_width;
+        ws.attach_workspace(p, device);
+        share_stage(p);
+        issue(observer, "lora_down", bytes,
+              [p, &context](bool) { hip_check(dlk_gemv(&p, context.stream), "LoRA down projection"); });
     }
 
     // 4's parameters first: when the output projection takes the tiled (prefill) path and the attention the

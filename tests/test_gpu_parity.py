@@ -572,6 +572,46 @@ def test_prefill_of_four_sequences_takes_the_tiled_projection_in_groups_of_four_
     assert rel_err(chunked, full) <= 1e-4
 
 
+@pytest.mark.parametrize("rank,batch", [(8, 4), (16, 4), (16, 16), (32, 4)])
+def test_decode_with_lora_down_rows_folded_into_the_qkv_launch(rank, batch):
+    # a decode step of 4..16 rows takes the few-row matrix-core QKV kernel, which at ranks 4..16 applies the LoRA
+    # down rows in its own key loop (rank 8: half the operand rows repeat and the up operand is zero past the
+    # rank); rank 32 keeps the separate down launch.  The prompt's prefill (more rows) takes the separate launch.
+    say(f"case: bf16 decode B={batch}, d=512, LoRA q/v rank {rank} (up weights 0.05 randn), f32 K/V")
+    cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=1024, context=64,
+                             dtype="bf16", lora_rank=rank, lora_alpha=2.0 * rank)
+    weights = oracle.synthesize_weights(cfg, (71, rank), 0.03)
+    ups = sorted(n for n in weights if "adapter.up" in n)
+    # up weights far above the synthesizer's 1e-3 randn, so the adapters move the logits well past the bound
+    for i, name in enumerate(ups):
+        weights[name] = oracle.bf16_encode(0.05 * oracle.randn((72, i), weights[name].size)).reshape(weights[name].shape)
+    ref, gpu = build_pair(cfg, weights=weights)
+    plain = oracle.OracleLM(cfg, {n: (np.zeros_like(v) if n in ups else v) for n, v in weights.items()})
+    P = 20
+    prompt = oracle.random_ids((73, rank), batch * P, cfg.vocab).reshape(batch, P)
+    rc, pc, gc = ref.make_cache(batch), plain.make_cache(batch), gpu.cache()
+    want = ref.logits(prompt, rc)[:, -1]
+    plain.logits(prompt, pc)
+    got = gpu.logits(prompt, gc)
+    assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4
+    ids = want.argmax(-1).reshape(batch, 1)
+    for step in range(3):
+        want = ref.logits(ids, rc)[:, -1]
+        without = plain.logits(ids, pc)[:, -1]
+        got = gpu.logits(ids, gc)
+        say(f"  step {step}: max|d| {np.max(np.abs(got - want)):.3g}, rel {rel_err(got, want):.3g}; "
+            f"the adapters' share rel {rel_err(without, want):.3g}")
+        assert rel_err(without, want) >= 20 * 5e-4, step  # a dropped or halved adapter term fails the bound
+        assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4, step
+        ids = want.argmax(-1).reshape(batch, 1)
+    # graph replay of the decode equals eager
+    gc.truncate(P + 3)
+    t1, l1 = gpu.generate(ids, 4, 0.0, (0, 0), use_graph=True, cache=gc)
+    gc.truncate(P + 3)
+    t2, l2 = gpu.generate(ids, 4, 0.0, (0, 0), use_graph=False, cache=gc)
+    assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
+
+
 def test_graph_decode_at_a_capacity_far_above_the_length_ignores_stale_workspace_memory():
     # graph replay sizes the key splits for the cache capacity, so most splits hold no keys and never write their
     # partial output rows; the merge must not read them.  The pool is first filled with NaN blocks and released, so
