@@ -288,7 +288,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
     uint32_t wfrag[2];
 #pragma unroll
     for (int sp = 0; sp < 2; ++sp) wfrag[sp] = (R / 8) * 1024 + (R % 8) * 128 + 16 * ((4 * sp + lane / 16) ^ (R >> 1));
-    auto compute = [&](const char* wbuf, int sp, const char* xbuf) {
+    // full: every weight tile of the column block exists, so the products need no per-tile check and form one
+    // basic block that the scheduler interleaves with the fragment reads (the check's branches split it)
+    auto compute = [&](const char* wbuf, int sp, const char* xbuf, auto full) {
+        constexpr bool FULL = decltype(full)::value;
         bf16x8 bh[4], bl[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -299,7 +302,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             // weight tiles past the end (a narrow launch) hold repeats of the last tile: no products for them
-            if (!SWIGLU && 16 * n_blk + slot_tile(i) >= tiles) continue;
+            if (!SWIGLU && !FULL && 16 * n_blk + slot_tile(i) >= tiles) continue;
             const bf16x8 a = *reinterpret_cast<const bf16x8*>(wbuf + slot_tile(i) * 2048 + wfrag[sp]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -333,31 +336,37 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
         wait_vm<0>();
     }
     ring_barrier();
-    int wb = 0; // buffer of the current pair
-    for (int c = 0; c < nsteps; c += 2) {
-        const int pair = c / 2;
-        const int wnext = wb == 0 ? kWeightStages - 1 : wb - 1; // pair + 2 takes the buffer of pair - 1
-        // even step c
-        if (!weight_wave) issue_acts(min(c + 1, nsteps - 1), xring[1]);
-        compute(wring[wb], 0, xring[0]);
-        if (weight_wave) {
-            issue_weights(min(pair + 2, npairs - 1), H0{}, wring[wnext]);
-        } else {
-            wait_vm<0>();
+    auto run = [&](auto full) {
+        int wb = 0; // buffer of the current pair
+        for (int c = 0; c < nsteps; c += 2) {
+            const int pair = c / 2;
+            const int wnext = wb == 0 ? kWeightStages - 1 : wb - 1; // pair + 2 takes the buffer of pair - 1
+            // even step c
+            if (!weight_wave) issue_acts(min(c + 1, nsteps - 1), xring[1]);
+            compute(wring[wb], 0, xring[0], full);
+            if (weight_wave) {
+                issue_weights(min(pair + 2, npairs - 1), H0{}, wring[wnext]);
+            } else {
+                wait_vm<0>();
+            }
+            ring_barrier();
+            // odd step c + 1
+            if (!weight_wave) issue_acts(min(c + 2, nsteps - 1), xring[0]);
+            compute(wring[wb], 1, xring[1], full);
+            if (weight_wave) {
+                issue_weights(min(pair + 2, npairs - 1), H1{}, wring[wnext]);
+                wait_vm<kWeightDma>();
+            } else {
+                wait_vm<0>();
+            }
+            ring_barrier();
+            wb = wb + 1 == kWeightStages ? 0 : wb + 1;
         }
-        ring_barrier();
-        // odd step c + 1
-        if (!weight_wave) issue_acts(min(c + 2, nsteps - 1), xring[0]);
-        compute(wring[wb], 1, xring[1]);
-        if (weight_wave) {
-            issue_weights(min(pair + 2, npairs - 1), H1{}, wring[wnext]);
-            wait_vm<kWeightDma>();
-        } else {
-            wait_vm<0>();
-        }
-        ring_barrier();
-        wb = wb + 1 == kWeightStages ? 0 : wb + 1;
-    }
+    };
+    if (SWIGLU || 16 * (n_blk + 1) <= tiles)
+        run(std::true_type{});
+    else
+        run(std::false_type{}); // the last column block of a launch whose tiles do not fill it
     wait_vm<0>();
 
     const bool norm = NORM && p.apply_norm;
@@ -438,8 +447,46 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
                     }
                 }
             }
+            // the operands of four tiles at a time (up rows, rotation, residual) are loaded before their first
+            // store: a load issued after a store waits for it (the outputs may alias the operands as far as the
+            // compiler knows), so loads between the stores would cost a memory round trip per tile, with the
+            // CU's matrix cores idle until the work-group ends (four, not eight: the QKV variant's registers)
 #pragma clang loop unroll(full)
-            for (int i = 0; i < 8; ++i) {
+            for (int half = 0; half < 2; ++half) {
+            u32x4 up_rows[4];
+            float4 residual[4];
+            float2 rot_c[4], rot_s[4];
+#pragma clang loop unroll(full)
+            for (int h = 0; h < 4; ++h) {
+                const int i = 4 * half + h;
+                up_rows[h] = u32x4{0u, 0u, 0u, 0u};
+                residual[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+                rot_c[h] = rot_s[h] = make_float2(0.f, 0.f);
+                const int tile = 16 * n_blk + 8 * wn + i;
+                if (tile >= tiles) continue;
+                const gemm::TileMap tm = gemm::locate<false>(p, tile);
+                if constexpr (EPI == DLK_EPI_QKV) {
+                    const bool vseg = tm.seg == 2;
+                    // lanes whose k slots are past the rank keep zeros (the padding of the up operand)
+                    if (lora_mfma && lane_k && tm.seg != 1 && (vseg ? p.lora_hidden[2] : p.lora_hidden[0]))
+                        up_rows[h] = *reinterpret_cast<const u32x4*>(
+                            static_cast<const uint16_t*>(vseg ? p.lora_up[2] : p.lora_up[0]) +
+                            static_cast<int64_t>(tm.n0 + lane % 16) * p.lora_rank + 8 * q);
+                    if (tm.seg < 2 && m < p.M) {
+                        const int64_t table = where.position * (p.head_dim / 2) + ((tm.n0 + 4 * q) % p.head_dim) / 2;
+                        rot_c[h] = *reinterpret_cast<const float2*>(p.cosine + table);
+                        rot_s[h] = *reinterpret_cast<const float2*>(p.sine + table);
+                    }
+                }
+                if constexpr (EPI == DLK_EPI_RESIDUAL) {
+                    if (m < p.M)
+                        residual[h] = *reinterpret_cast<const float4*>(p.residual + static_cast<int64_t>(m) * p.ldres +
+                                                                       tm.n0 + 4 * q);
+                }
+            }
+#pragma clang loop unroll(full)
+            for (int h = 0; h < 4; ++h) {
+                const int i = 4 * half + h;
                 const int tile = 16 * n_blk + 8 * wn + i;
                 if (tile >= tiles) continue; // wave-uniform: the MFMA below takes operands from every lane
                 const gemm::TileMap tm = gemm::locate<false>(p, tile);
@@ -451,11 +498,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
                 if constexpr (EPI == DLK_EPI_QKV) {
                     const bool vseg = tm.seg == 2;
                     if (lora_mfma && tm.seg != 1 && (vseg ? p.lora_hidden[2] : p.lora_hidden[0])) {
-                        const uint16_t* up = static_cast<const uint16_t*>(vseg ? p.lora_up[2] : p.lora_up[0]) +
-                                             static_cast<int64_t>(tm.n0 + lane % 16) * p.lora_rank + 8 * (lane_k ? q : 0);
-                        u32x4 raw = *reinterpret_cast<const u32x4*>(up);
-                        if (!lane_k) raw = u32x4{0u, 0u, 0u, 0u};
-                        const bf16x8 a = __builtin_bit_cast(bf16x8, raw);
+                        const bf16x8 a = __builtin_bit_cast(bf16x8, up_rows[h]);
                         f32x4 d = {0.f, 0.f, 0.f, 0.f};
                         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, vseg ? hh[1] : hh[0], d, 0, 0, 0);
                         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, vseg ? hl[1] : hl[0], d, 0, 0, 0);
@@ -469,7 +512,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
                         const int n = (EPI == DLK_EPI_STORE ? gemv::seg_column(p, tm.seg) : 0) + tm.n0 + 4 * q;
                         float4 out = make_float4(v[0], v[1], v[2], v[3]);
                         if constexpr (EPI == DLK_EPI_RESIDUAL) {
-                            const float4 r = *reinterpret_cast<const float4*>(p.residual + static_cast<int64_t>(m) * p.ldres + n);
+                            const float4 r = residual[h];
                             out.x += r.x; out.y += r.y; out.z += r.z; out.w += r.w;
                         }
                         *reinterpret_cast<float4*>(p.y + static_cast<int64_t>(m) * p.ldy + n) = out;
@@ -490,9 +533,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
                         continue; // ranks the MFMA pair does not take: the scalar path
                     }
                     if (tm.seg < 2) {
-                        const int64_t table = where.position * (hd / 2) + d / 2;
-                        const float2 c = *reinterpret_cast<const float2*>(p.cosine + table);
-                        const float2 sn = *reinterpret_cast<const float2*>(p.sine + table);
+                        const float2 c = rot_c[h], sn = rot_s[h];
                         const float e0 = o[0] * c.x - o[1] * sn.x, o0 = o[0] * sn.x + o[1] * c.x;
                         const float e1 = o[2] * c.y - o[3] * sn.y, o1 = o[2] * sn.y + o[3] * c.y;
                         o[0] = e0; o[1] = o0; o[2] = e1; o[3] = o1;
@@ -512,6 +553,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
                     continue;
                 }
                 gemm::lane_epilogue<EPI>(p, tm, q, m, v, bs, bi, p.key_seed, p.key_stream, lora, where);
+            }
             }
         }
     }
