@@ -299,15 +299,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
             bh[j] = *reinterpret_cast<const bf16x8*>(frag);
             bl[j] = *reinterpret_cast<const bf16x8*>(frag + 1024);
         }
+        // all eight weight fragments before the products (the LDS slots of tiles past the end hold repeats of
+        // the last tile, so every read is in bounds)
+        bf16x8 a[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const bf16x8*>(wbuf + slot_tile(i) * 2048 + wfrag[sp]);
+        __builtin_amdgcn_sched_barrier(0); // keeps the scheduler from sinking the reads to their first use
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            // weight tiles past the end (a narrow launch) hold repeats of the last tile: no products for them
+            // weight tiles past the end (a narrow launch): no products for them
             if (!SWIGLU && !FULL && 16 * n_blk + slot_tile(i) >= tiles) continue;
-            const bf16x8 a = *reinterpret_cast<const bf16x8*>(wbuf + slot_tile(i) * 2048 + wfrag[sp]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh[j], acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bh[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bl[j], acc[i][j], 0, 0, 0);
             }
         }
     };
