@@ -42,9 +42,9 @@ constexpr int kPrepThreads = 256;                  // prepare_rows: one work-gro
 constexpr int kPrepChunk = 512;                    // k per prepare_rows work-group
 constexpr int kBN = 256;                           // weight rows per work-group (16 tiles of 16)
 constexpr int kBM = 256;                           // activation rows per work-group (16 tiles of 16)
-constexpr int kActStages = 2;                      // activation ring: k steps of 32
+constexpr int kActStages = 3;                      // activation ring: k steps of 32
 constexpr int kActBytes = (kBM / 16) * 2048;       // one k step of activation fragments (hi, lo)
-constexpr int kWeightStages = 3;                   // weight ring: k pairs (64)
+constexpr int kWeightStages = 2;                   // weight ring: k pairs (64)
 constexpr int kWeightPairBytes = (kBN / 16) * 2048; // one k pair of weight fragments
 constexpr size_t kLdsBytes = 0;                    // the rings are static LDS
 constexpr int kActDma = 2 * (kBM / 16) / (kWaves / 2);   // activation DMA instructions per activation wave per k step
@@ -317,55 +317,55 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_tiles(const dlk_gemv_params 
         }
     };
 
-    // Two rings.  Weights: three buffers of one k pair.  A weight wave issues pair p + 2 in two halves, after its
-    // products of steps 2p and 2p + 1, into the buffer of pair p - 1 (which every wave finished before the
-    // barrier of step 2p), and at the end of step 2p + 1 waits until only those DMAs are in flight, so pair p + 1
-    // has landed before the barrier of step 2p + 2: about four k steps of lead for the operand that comes from
-    // the last-level cache or HBM.  Activations: two buffers of one k step; an activation wave issues
-    // step c + 1 right after the barrier of step c (into the buffer of step c - 1) and waits for it before the
-    // next barrier: one step of lead for rows that a group of work-groups shares in its L2.  Issues past the end
-    // repeat the last pair or step into a buffer nobody reads again, keeping the counts uniform.  A SIMD holds
-    // waves w and w + 4, one of each kind, so one issues its DMAs before its products and the other after them.
-    // nsteps is even.
+    // Two rings.  Activations: three buffers of one k step; an activation wave issues step c + 2 right after
+    // the barrier of step c (into the buffer of step c - 1, which every wave finished before that barrier) and
+    // before the next barrier waits until only those DMAs are in flight, so step c + 1 has landed: two steps of
+    // lead.  Weights: two buffers of one k pair; a weight wave issues pair p + 1 after its products of step 2p,
+    // into the buffer of pair p - 1, and waits for it at the end of step 2p + 1: about one and a half steps of
+    // lead.  (The other split of the 160 KB, three weight pairs two pairs ahead and two activation steps one
+    // ahead, measured slower: the activation slices the work-groups of a group share wait on each other's L2
+    // misses.)  Issues past the end repeat the last pair or step into a buffer nobody reads again, keeping the
+    // counts uniform.  A SIMD holds waves w and w + 4, one of each kind, so one issues its DMAs before its
+    // products and the other after them.  nsteps is even.
     const int npairs = nsteps / 2;
     using H0 = std::integral_constant<int, 0>;
     using H1 = std::integral_constant<int, 1>;
     if (weight_wave) {
         issue_weights(0, H0{}, wring[0]);
         issue_weights(0, H1{}, wring[0]);
-        issue_weights(min(1, npairs - 1), H0{}, wring[1]);
-        issue_weights(min(1, npairs - 1), H1{}, wring[1]);
-        wait_vm<kWeightDma>();
+        wait_vm<0>();
     } else {
         issue_acts(0, xring[0]);
-        wait_vm<0>();
+        issue_acts(min(1, nsteps - 1), xring[1]);
+        wait_vm<kActDma>();
     }
     ring_barrier();
     auto run = [&](auto full) {
-        int wb = 0; // buffer of the current pair
+        int wb = 0, xs = 0; // buffers of the current pair and of its first step
         for (int c = 0; c < nsteps; c += 2) {
             const int pair = c / 2;
-            const int wnext = wb == 0 ? kWeightStages - 1 : wb - 1; // pair + 2 takes the buffer of pair - 1
+            const int x1 = xs == 2 ? 0 : xs + 1, x2 = x1 == 2 ? 0 : x1 + 1;
             // even step c
-            if (!weight_wave) issue_acts(min(c + 1, nsteps - 1), xring[1]);
-            compute(wring[wb], 0, xring[0], full);
+            if (!weight_wave) issue_acts(min(c + 2, nsteps - 1), xring[x2]);
+            compute(wring[wb], 0, xring[xs], full);
             if (weight_wave) {
-                issue_weights(min(pair + 2, npairs - 1), H0{}, wring[wnext]);
+                issue_weights(min(pair + 1, npairs - 1), H0{}, wring[1 - wb]);
+                issue_weights(min(pair + 1, npairs - 1), H1{}, wring[1 - wb]);
             } else {
-                wait_vm<0>();
+                wait_vm<kActDma>();
             }
             ring_barrier();
-            // odd step c + 1
-            if (!weight_wave) issue_acts(min(c + 2, nsteps - 1), xring[0]);
-            compute(wring[wb], 1, xring[1], full);
+            // odd step c + 1 (step c + 3 takes the buffer of step c)
+            if (!weight_wave) issue_acts(min(c + 3, nsteps - 1), xring[xs]);
+            compute(wring[wb], 1, xring[x1], full);
             if (weight_wave) {
-                issue_weights(min(pair + 2, npairs - 1), H1{}, wring[wnext]);
-                wait_vm<kWeightDma>();
-            } else {
                 wait_vm<0>();
+            } else {
+                wait_vm<kActDma>();
             }
             ring_barrier();
-            wb = wb + 1 == kWeightStages ? 0 : wb + 1;
+            wb = 1 - wb;
+            xs = x2;
         }
     };
     if (SWIGLU || 16 * (n_blk + 1) <= tiles)
