@@ -612,6 +612,38 @@ def test_decode_with_lora_down_rows_folded_into_the_qkv_launch(rank, batch):
     assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
 
 
+@pytest.mark.parametrize("batch", [4, 16])
+def test_decode_with_lora_folded_at_the_c5_width(batch):
+    # the C5 layer (d = 2048, 32/8 heads, F = 5632, rank 16): each of the QKV launch's 16 waves takes 128 keys, four
+    # k steps of the down rows in one batch of loads
+    say(f"case: bf16 decode B={batch}, one C5-width layer, LoRA q/v rank 16 (up weights 0.05 randn), f32 K/V")
+    cfg = oracle.ModelConfig(vocab=512, layers=1, dimensions=2048, heads=32, kv_heads=8, hidden=5632, context=40,
+                             dtype="bf16", lora_rank=16, lora_alpha=32.0)
+    weights = oracle.synthesize_weights(cfg, (74, batch), 0.02)
+    ups = sorted(n for n in weights if "adapter.up" in n)
+    for i, name in enumerate(ups):
+        weights[name] = oracle.bf16_encode(0.05 * oracle.randn((75, i), weights[name].size)).reshape(weights[name].shape)
+    ref, gpu = build_pair(cfg, weights=weights)
+    plain = oracle.OracleLM(cfg, {n: (np.zeros_like(v) if n in ups else v) for n, v in weights.items()})
+    P = 12
+    prompt = oracle.random_ids((76, batch), batch * P, cfg.vocab).reshape(batch, P)
+    rc, pc, gc = ref.make_cache(batch), plain.make_cache(batch), gpu.cache()
+    want = ref.logits(prompt, rc)[:, -1]
+    plain.logits(prompt, pc)
+    got = gpu.logits(prompt, gc)
+    assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4
+    ids = want.argmax(-1).reshape(batch, 1)
+    for step in range(3):
+        want = ref.logits(ids, rc)[:, -1]
+        without = plain.logits(ids, pc)[:, -1]
+        got = gpu.logits(ids, gc)
+        say(f"  step {step}: max|d| {np.max(np.abs(got - want)):.3g}, rel {rel_err(got, want):.3g}; "
+            f"the adapters' share rel {rel_err(without, want):.3g}")
+        assert rel_err(without, want) >= 20 * 5e-4, step
+        assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4, step
+        ids = want.argmax(-1).reshape(batch, 1)
+
+
 def test_graph_decode_at_a_capacity_far_above_the_length_ignores_stale_workspace_memory():
     # graph replay sizes the key splits for the cache capacity, so most splits hold no keys and never write their
     # partial output rows; the merge must not read them.  The pool is first filled with NaN blocks and released, so
