@@ -424,26 +424,50 @@ __global__ __launch_bounds__(kThreads, sizeof(KT) == 2 ? 2 : 1) void attention_p
                 l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, ph[u][qt], l[qt], 0, 0, 0);
                 l[qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pl[u][qt], l[qt], 0, 0, 0);
             }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+        auto v_frag = [&](int plane, int dt, int u) {
+            const int at = (16 * dt + lane % 16) * VSTRIDE + 32 * u + 4 * q;
+            const u32x2 lo4 = *reinterpret_cast<const u32x2*>(&vt[plane][buf][at]);
+            const u32x2 hi4 = *reinterpret_cast<const u32x2*>(&vt[plane][buf][at + 16]);
+            return __builtin_bit_cast(bf16x8, u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
+        };
+        if constexpr (HD == 64) {
+            // one key half at a time: its V^T fragments of every head-dim tile are read before its products (a
+            // scheduling barrier keeps the reads from sinking to their first use, where each would expose an LDS
+            // latency); each o[qt][dt] still takes half 0, then half 1.  At head dim 128 the registers would spill.
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const int at = (16 * dt + lane % 16) * VSTRIDE + 32 * u + 4 * q;
-                const u32x2 lo4 = *reinterpret_cast<const u32x2*>(&vt[0][buf][at]);
-                const u32x2 hi4 = *reinterpret_cast<const u32x2*>(&vt[0][buf][at + 16]);
-                const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
-                bf16x8 al;
-                if constexpr (F32) {
-                    const u32x2 llo4 = *reinterpret_cast<const u32x2*>(&vt[PLANES - 1][buf][at]);
-                    const u32x2 lhi4 = *reinterpret_cast<const u32x2*>(&vt[PLANES - 1][buf][at + 16]);
-                    al = __builtin_bit_cast(bf16x8, u32x4{llo4.x, llo4.y, lhi4.x, lhi4.y});
-                }
+                bf16x8 a[DT], al[DT];
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) {
-                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[u][qt], o[qt][dt], 0, 0, 0);
-                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[u][qt], o[qt][dt], 0, 0, 0);
-                    if constexpr (F32)
-                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ph[u][qt], o[qt][dt], 0, 0, 0);
+                for (int dt = 0; dt < DT; ++dt) {
+                    a[dt] = v_frag(0, dt, u);
+                    if constexpr (F32) al[dt] = v_frag(PLANES - 1, dt, u);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) {
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[dt], ph[u][qt], o[qt][dt], 0, 0, 0);
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[dt], pl[u][qt], o[qt][dt], 0, 0, 0);
+                        if constexpr (F32)
+                            o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[dt], ph[u][qt], o[qt][dt], 0, 0, 0);
+                    }
+            }
+        } else {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const bf16x8 a = v_frag(0, dt, u);
+                    bf16x8 al;
+                    if constexpr (F32) al = v_frag(PLANES - 1, dt, u);
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) {
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ph[u][qt], o[qt][dt], 0, 0, 0);
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pl[u][qt], o[qt][dt], 0, 0, 0);
+                        if constexpr (F32)
+                            o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, ph[u][qt], o[qt][dt], 0, 0, 0);
+                    }
                 }
             }
         }
