@@ -572,11 +572,12 @@ def test_prefill_of_four_sequences_takes_the_tiled_projection_in_groups_of_four_
     assert rel_err(chunked, full) <= 1e-4
 
 
-@pytest.mark.parametrize("rank,batch", [(8, 4), (16, 4), (16, 16), (32, 4)])
+@pytest.mark.parametrize("rank,batch", [(8, 4), (16, 4), (16, 16), (32, 4), (16, 32)])
 def test_decode_with_lora_down_rows_folded_into_the_qkv_launch(rank, batch):
     # a decode step of 4..16 rows takes the few-row matrix-core QKV kernel, which at ranks 4..16 applies the LoRA
     # down rows in its own key loop (rank 8: half the operand rows repeat and the up operand is zero past the
-    # rank); rank 32 keeps the separate down launch.  The prompt's prefill (more rows) takes the separate launch.
+    # rank); rank 32, and 32 rows (the key-split kernel), keep the separate down launch.  The prompt's prefill
+    # (more rows) takes the separate launch.
     say(f"case: bf16 decode B={batch}, d=512, LoRA q/v rank {rank} (up weights 0.05 randn), f32 K/V")
     cfg = oracle.ModelConfig(vocab=512, layers=2, dimensions=512, heads=8, kv_heads=2, hidden=1024, context=64,
                              dtype="bf16", lora_rank=rank, lora_alpha=2.0 * rank)
@@ -610,6 +611,36 @@ def test_decode_with_lora_down_rows_folded_into_the_qkv_launch(rank, batch):
     gc.truncate(P + 3)
     t2, l2 = gpu.generate(ids, 4, 0.0, (0, 0), use_graph=False, cache=gc)
     assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
+
+
+def test_tiled_prefill_with_lora_and_a_partial_qkv_column_block():
+    # d = 256, 8/2 heads of 32: the QKV projection has 24 weight tiles, one full column block of 16 and one of 8,
+    # which runs the tiled kernel's checked products and its LoRA epilogue on the missing tiles' slots
+    say("case: bf16 prefill B=2 x 512, d=256 (QKV 384 columns: a partial column block), LoRA q/v rank 16, f32 K/V")
+    cfg = oracle.ModelConfig(vocab=256, layers=2, dimensions=256, heads=8, kv_heads=2, hidden=512, context=520,
+                             dtype="bf16", lora_rank=16, lora_alpha=32.0)
+    weights = oracle.synthesize_weights(cfg, (77, 0), 0.05)
+    ups = sorted(n for n in weights if "adapter.up" in n)
+    for i, name in enumerate(ups):
+        weights[name] = oracle.bf16_encode(0.05 * oracle.randn((78, i), weights[name].size)).reshape(weights[name].shape)
+    ref, gpu = build_pair(cfg, weights=weights)
+    plain = oracle.OracleLM(cfg, {n: (np.zeros_like(v) if n in ups else v) for n, v in weights.items()})
+    B, P = 2, 512
+    prompt = oracle.random_ids((79, 0), B * P, cfg.vocab).reshape(B, P)
+    rc, gc = ref.make_cache(B), gpu.cache()
+    want = ref.logits(prompt, rc)[:, -1]
+    without = plain.logits(prompt, plain.make_cache(B))[:, -1]
+    got = gpu.logits(prompt, gc)
+    say(f"  prefill logits: max|d| {np.max(np.abs(got - want)):.3g}, rel {rel_err(got, want):.3g}; "
+        f"the adapters' share rel {rel_err(without, want):.3g}")
+    assert rel_err(without, want) >= 20 * 5e-4
+    assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4
+    ids = want.argmax(-1).reshape(B, 1)
+    for step in range(2):  # decode over the keys the tiled QKV epilogue wrote
+        want = ref.logits(ids, rc)[:, -1]
+        got = gpu.logits(ids, gc)
+        assert np.max(np.abs(got - want)) <= 2e-2 and rel_err(got, want) <= 5e-4, step
+        ids = want.argmax(-1).reshape(B, 1)
 
 
 @pytest.mark.parametrize("batch", [4, 16])
