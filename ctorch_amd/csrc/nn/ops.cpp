@@ -89,16 +89,16 @@ void attention_split(Index batch, Index heads, Index kv_heads, Index head_dim, b
         // waves per work-group when the keys split).  With 256 or more (sequence, KV head) pairs there is a
         // work-group per pair already, so each takes all of its keys (no partials, no combine launch: C3); an
         // f32 cache of at most 512 keys stays in one work-group per pair (C2: eight waves); otherwise runs of
-        // 64..256 keys per wave, about total / 1024 keys over a bf16 cache and total / 512 over an f32 cache
-        // (measured on MI355X at b=4 over 4100 keys: bf16 14.6 us per layer at 192 keys per wave against 15.8 at
-        // 64 and 256; f32 23.8 us at 256 against 26.5 at 128; C4 keeps 256)
+        // 64..256 keys per wave, about total / 1024 keys (measured on MI355X at b=4 over 4100 keys: bf16 14.6 us
+        // per layer at 192 keys per wave against 15.8 at 64 and 256; f32 19.8 us at 192 against 22.9 at 256 and
+        // 25.8 at 128; C4 keeps 256)
         const Index total = batch * kv_heads * source;
         if (batch * kv_heads >= 256) {
             chunk = static_cast<int>(4 * (((source + 3) / 4 + 63) / 64 * 64));
         } else if (!kv_bf16 && source <= DLK_DECODE_CHUNK_MAX) {
             chunk = DLK_DECODE_CHUNK_MAX;
         } else {
-            const Index per_run = kv_bf16 ? 1024 : 512;
+            const Index per_run = 1024;
             chunk = static_cast<int>(4 * std::clamp<Index>(((total + per_run - 1) / per_run + 63) / 64 * 64, 64, 256));
         }
         splits = static_cast<int>((source + chunk - 1) / chunk);
