@@ -502,8 +502,8 @@ int launch(const dlk_attention_params& p, hipStream_t stream) {
     // one short chunk per (sequence, KV head) (a one-sequence decode: one work-group per KV head) spreads over
     // eight waves; key splits and long runs over four (measured on MI355X: 1B widths, f32 cache, 129 / 257 / 385
     // keys: 6.1 / 7.6 / 10.3 us per layer with eight, 7.9 / 8.4 / 9.2 with four; batch 32 over 2048 bf16 keys:
-    // 25.7 us with four, 26.4 with eight; batch 4 over 4100 keys in 512-key splits: 26.5 us with four, 28.5 with
-    // eight, and in the 1024-key splits the policy takes for an f32 cache: 23.0 with four, 24.1 with eight)
+    // 25.7 us with four, 26.4 with eight; batch 4 over 4100 keys of an f32 cache in 512-key splits: 26.5 us with
+    // four, 28.5 with eight, and in 1024-key splits: 23.0 with four, 24.1 with eight)
     if constexpr (HD == 64) {
         if (p.chunk <= 512 && p.splits == 1) {
             if (p.qkv_partial) hipLaunchKernelGGL((attention_matrix<KT, HD, 8, true>), grid, dim3(8 * kWave), 0, stream, p);
