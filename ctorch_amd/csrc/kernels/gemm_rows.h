@@ -100,8 +100,12 @@ inline int splits_of(const dlk_gemv_params& p, int rows) {
     const int blocks = blocks_of(p);
     if (blocks >= 192) return 1;
     const int chunks = p.K / chunk_k(row_tiles(rows));
+    // SwiGLU over at most 16 rows (a small batch's gate/up) within 720 work-groups: at batch 4, 8 slices (704
+    // work-groups) 14.6-14.7 us against 15.7 at 4 and 15.9 at 16, the C5 decode step 1.030 -> 1.011 ms (A/B,
+    // interleaved runs).  The other launches keep the cap their split counts were measured at.
+    const int cap = p.epilogue == DLK_EPI_SWIGLU && rows <= 16 ? 720 : 352;
     int best = 1;
-    for (int s = 2; s <= kMaxSplits && blocks * s <= 352; ++s) {
+    for (int s = 2; s <= kMaxSplits && blocks * s <= cap; ++s) {
         if (chunks % s == 0) best = s;
     }
     return best;
